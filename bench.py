@@ -1,0 +1,183 @@
+"""Benchmark: MAXIM-3S forward pass on one MI355X.
+
+One step = one MAXIM-3S forward pass (2885 ops) over one 600x400 RGB image
+reflect-padded to 640x448, with the image and the weights already resident
+in HBM when the timed region starts. Prints ONE JSON line:
+
+  value         images/s (whole job; one GPU)
+  ms_per_step   ms/image
+  roofline      the dominant kernel family's achieved rate against its bound
+                (fp32 MFMA 157.3 TFLOP/s or HBM 8 TB/s), from HIP events on the
+                executor's stream over the timed region
+  cpu_baseline  the CPU path (oracle/, a C restatement of the reference's
+                src/exec_cpu.rs) timed on this host over one full pass
+
+  python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
+"""
+
+import argparse
+import collections
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+for p in (os.path.join(ROOT, "maxim-rs_amd"), ROOT):
+    if p not in sys.path:
+        sys.path.insert(0, p)
+
+import numpy as np  # noqa: E402
+
+METRIC = "ms/image & images/s, MAXIM-3S 640x448 fp32; GEMM % of MFMA peak, HBM GB/s"
+SEED = 1
+GAIN = 0.3
+
+
+def smooth_image(h, w, seed=0, noise=0.1):
+    rng = np.random.default_rng(seed)
+    y, x = np.mgrid[0:h, 0:w].astype(np.float64)
+    img = np.empty((3, h, w))
+    for c in range(3):
+        f = rng.uniform(0.5, 3.0, size=(3, 2))
+        ph = rng.uniform(0, 2 * np.pi, size=3)
+        v = 0.5 + sum(0.1 * np.sin(2 * np.pi * (f[k, 0] * y / h + f[k, 1] * x / w) + ph[k]) for k in range(3))
+        img[c] = v + rng.normal(0, noise, size=(h, w))
+    return np.clip(img, 0, 1).astype(np.float32)
+
+
+def family(kernel):
+    """Group kernel entry points into the family a roofline is quoted for."""
+    for pre in ("mx_gemm", "mx_conv3x3", "mx_conv4x4", "mx_chan_ln", "mx_block_perm", "mx_resize",
+                "mx_chan_mean", "mx_gemv"):
+        if kernel.startswith(pre):
+            return pre
+    return kernel.rsplit("_", 1)[0] if kernel.endswith(("_v4", "_s")) else kernel
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--cpu-threads", type=int, default=min(16, os.cpu_count() or 1))
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py: this build runs on one GPU only (a MAXIM pass is one image on one device; "
+              "data-parallel serving is N independent processes). Use --gpus 1.", file=sys.stderr)
+        sys.exit(2)
+
+    from maxim_amd import plan as P
+    from maxim_amd import hip as H
+    from maxim_amd import roofline as R
+
+    w = P.Weights.synthetic("S-3", seed=SEED, gain=GAIN, bias_std=0.02, ln_std=0.1)
+    raw = smooth_image(400, 600, seed=4)
+    pad = P.preprocess(raw, 64)
+    _, ph, pw = pad.img.shape
+    plan = P.Plan(w, ph, pw)
+    n_ops = len(plan.ops)
+    print("bench: MAXIM-3S %dx%d, %d ops, arena %.1f MiB" % (pw, ph, n_ops, plan.arena_bytes / 2**20),
+          file=sys.stderr, flush=True)
+
+    gpu = H.Gpu(plan)
+    # PCIe-inclusive pass (input H2D, ops, output D2H), reported on stderr only.
+    t0 = time.perf_counter()
+    out = gpu.run(pad.img)
+    e2e_first = time.perf_counter() - t0
+    assert np.isfinite(out).all(), "non-finite output"
+    for _ in range(args.warmup):
+        gpu.run_ops(0, n_ops)
+    gpu.sync()
+
+    # Timed region: K passes over the resident image, per-op HIP events on the
+    # executor's stream (the timeline), bracketed by device synchronisation.
+    per_kernel = collections.defaultdict(lambda: [0.0, 0, 0.0, 0.0])  # ms, launches, flops, bytes
+    step_ms = []
+    gpu.sync()
+    t_start = time.perf_counter()
+    for _ in range(args.steps):
+        ms = gpu.run_timed()
+        step_ms.append(ms[1])
+        for i, op in enumerate(plan.ops):
+            fam = family(gpu.op_kernel(i))
+            f, b = R.op_cost(op)
+            e = per_kernel[fam]
+            e[0] += float(ms[0][i])
+            e[1] += 1
+            e[2] += f
+            e[3] += b
+    gpu.sync()
+    wall = time.perf_counter() - t_start
+    ms_per_step = wall * 1e3 / args.steps
+    ev_ms = float(np.median(step_ms))
+
+    # Dominant family by device time; its bound decides the roofline axis.
+    fam, (tms, nl, fl, by) = max(per_kernel.items(), key=lambda kv: kv[1][0])
+    avg_s = tms / nl / 1e3
+    ai = fl / by if by else 0.0
+    if ai >= R.RIDGE:
+        roof = {"bound": "mfma", "achieved": fl / nl / avg_s / 1e12, "peak": 157.3, "unit": "TFLOP/s"}
+    else:
+        roof = {"bound": "hbm", "achieved": by / nl / avg_s / 1e9, "peak": 8000.0, "unit": "GB/s"}
+    roof["frac"] = roof["achieved"] / roof["peak"]
+    roof["traffic"] = None
+    roof["kernel"] = fam
+    roof["avg_launch_us"] = avg_s * 1e6
+    roof["launches_per_step"] = nl // args.steps
+
+    fl_all, by_all, bound_s = R.plan_cost(plan)
+    print("bench: %.3f ms/image wall, %.3f ms event-timed (roofline sum of per-op bounds %.2f ms)"
+          % (ms_per_step, ev_ms, bound_s * 1e3), file=sys.stderr)
+    print("bench: first pass incl. H2D/D2H and launch setup %.1f ms" % (e2e_first * 1e3), file=sys.stderr)
+    tot = sum(v[0] for v in per_kernel.values())
+    for k, (t, n, f, b) in sorted(per_kernel.items(), key=lambda kv: -kv[1][0]):
+        avg = t / n / 1e3
+        print("  %-20s %5.1f%%  %4d launches/step  avg %7.1f us  %7.2f TFLOP/s  %7.1f GB/s"
+              % (k, 100 * t / tot, n // args.steps, avg * 1e6, f / n / avg / 1e12, b / n / avg / 1e9),
+              file=sys.stderr)
+
+    cpu = None
+    if not args.no_cpu:
+        cpu = cpu_baseline(plan, pad.img, args.cpu_threads)
+
+    line = {
+        "metric": METRIC,
+        "value": 1e3 / ms_per_step,
+        "unit": "images/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms_per_step,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp32",
+        "data": "synthetic: seeded He-normal x0.3 weights, 600x400 smooth pattern + N(0,0.1) image",
+        "config": {"workload": "C4: MAXIM-3S, 600x400 RGB reflect-padded to 640x448, one image per step",
+                   "variant": "S-3", "ops": n_ops, "arena_mib": round(plan.arena_bytes / 2**20, 1),
+                   "gflop_per_image": round(fl_all / 1e9, 1), "gb_per_image": round(by_all / 1e9, 2),
+                   "sum_of_op_bounds_ms": round(bound_s * 1e3, 2)},
+        "roofline": roof,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+
+
+def cpu_baseline(plan, img, threads):
+    """The CPU path over one full pass of the same plan and image."""
+    from oracle import oracle as O
+    arena = np.zeros(plan.arena_len, np.float32)
+    o = int(plan.offs[plan.input])
+    arena[o:o + img.size] = img.ravel()
+    t0 = time.perf_counter()
+    O.run(plan, arena, threads)
+    dt = time.perf_counter() - t0
+    return {"value": 1.0 / dt, "unit": "images/s", "cores": O.threads_used(), "kind": "port",
+            "sample": "one full MAXIM-3S 640x448 pass (2885 ops) of the C restatement of "
+                      "src/exec_cpu.rs, %.1f s" % dt}
+
+
+if __name__ == "__main__":
+    main()

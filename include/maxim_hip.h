@@ -1,0 +1,98 @@
+/*
+ * maxim_hip.h - the MI355X (gfx950) executor for a MAXIM plan.
+ *
+ * The C-ABI form of the reference's GPU executor, `exec_gpu::Gpu`
+ * (src/exec_gpu.rs:48-357), standing beside it as a third executor behind the
+ * same plan/arena/weights interface (maxim_plan.h's `mx_plan_desc`). The HIP
+ * runtime is dlopen'd (`libamdhip64.so`), the way src/cuda.rs reaches
+ * libcuda through lightgpu; the gfx950 code object is embedded in this
+ * library and loaded with hipModuleLoadData.
+ *
+ * Ownership: the executor owns exactly one device arena of `arena_len` floats
+ * and a device copy of the weights (uploaded eagerly by mxh_new, in the
+ * layouts its kernels read). Plans and host buffers are borrowed per call.
+ * The arena is NOT zeroed: every buffer is written before it is read.
+ * Errors: negative status / NULL, message in mx_last_error() (thread-local).
+ * Threading: one executor per thread; launches are asynchronous on the
+ * executor's own stream and every call that returns host data synchronises.
+ */
+#ifndef MAXIM_HIP_H
+#define MAXIM_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#include "maxim_plan.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct mxh_gpu mxh_gpu;
+
+/* exec_gpu::driver_ready (src/exec_gpu.rs:81-83): dlopen the HIP runtime and
+ * bring device 0 up. The only failure that lets a caller choose another
+ * backend; anything after this is reported, never retried elsewhere. */
+int mxh_driver_ready(void);
+
+/* Gpu::new (src/exec_gpu.rs:96-160): load the kernels, size the pass against
+ * free device memory and REFUSE (with the numbers) if arena + weights do not
+ * fit, then allocate the arena and upload the weights. */
+mxh_gpu *mxh_new(const mx_plan_desc *plan);
+void mxh_free(mxh_gpu *g);
+
+/* Gpu::run (src/exec_gpu.rs:196-229): input in, every op, output out. */
+int mxh_run(mxh_gpu *g, const mx_plan_desc *plan, const float *input, uint64_t n_in, float *output,
+            uint64_t n_out);
+/* Gpu::begin (src/exec_gpu.rs:313-344): place the input image in the arena. */
+int mxh_begin(mxh_gpu *g, const mx_plan_desc *plan, const float *input, uint64_t n_in);
+/* Gpu::step_op (src/exec_gpu.rs:346-351): execute exactly op `i`. */
+int mxh_step_op(mxh_gpu *g, const mx_plan_desc *plan, uint64_t i);
+/* All ops [first, last) in order, asynchronously (no host synchronisation). */
+int mxh_run_ops(mxh_gpu *g, const mx_plan_desc *plan, uint64_t first, uint64_t last);
+/* Gpu::read_buf (src/exec_gpu.rs:353-357): one buffer back to the host. */
+int mxh_read_buf(mxh_gpu *g, const mx_plan_desc *plan, uint64_t buf, float *out, uint64_t n);
+/* Gpu::read_into / read_arena (src/exec_gpu.rs:285-300): `n` floats from arena element `off`. */
+int mxh_read_into(mxh_gpu *g, uint64_t off, float *out, uint64_t n);
+int mxh_read_arena(mxh_gpu *g, float *out, uint64_t n);
+/* The inverse of mxh_read_into (Gpu::write_at, src/exec_gpu.rs:272-281): used
+ * by the per-op parity walk to give an op exactly the CPU path's inputs. */
+int mxh_write_into(mxh_gpu *g, uint64_t off, const float *in, uint64_t n);
+/* MAXIM_POISON (src/exec_gpu.rs:313-340): fill the whole arena with 0xCD bytes. */
+int mxh_poison(mxh_gpu *g);
+/* Wait for all queued work. */
+int mxh_sync(mxh_gpu *g);
+
+/* Gpu::set_timeline / timeline (src/exec_gpu.rs:176-194, 231-265): with the
+ * timeline on, mxh_run records one HIP event per op and reports per-op device
+ * milliseconds, synchronising once at the end. */
+void mxh_set_timeline(mxh_gpu *g, int on);
+int mxh_timeline(mxh_gpu *g, float *per_op_ms, uint64_t n, float *total_ms);
+/* Gpu::run_timed (src/exec_gpu.rs:241-265) without the copies: every op over
+ * the image already in the arena, one event per op, one synchronisation. */
+int mxh_run_timed(mxh_gpu *g, const mx_plan_desc *plan);
+
+/* Time `iters` passes of ops [first, last) back to back with HIP events on
+ * the executor's stream; `ms` gets the total device time. */
+int mxh_time_ops(mxh_gpu *g, const mx_plan_desc *plan, uint64_t first, uint64_t last, int iters,
+                 float *ms);
+
+/* Gpu::device_name / arena_bytes / weight_bytes / pool_bytes / ops_launched
+ * (src/exec_gpu.rs:162-175). kernels_launched counts launches (one op may be
+ * several, e.g. the two resize passes). */
+const char *mxh_device_name(mxh_gpu *g);
+uint64_t mxh_arena_bytes(mxh_gpu *g);
+uint64_t mxh_weight_bytes(mxh_gpu *g);
+uint64_t mxh_pool_bytes(mxh_gpu *g);
+uint64_t mxh_ops_launched(mxh_gpu *g);
+uint64_t mxh_kernels_launched(mxh_gpu *g);
+/* The name of the first kernel op `i` launches (for per-kernel reports). */
+const char *mxh_op_kernel(mxh_gpu *g, uint64_t i);
+/* Device facts for the roofline: compute units and peak engine clock (kHz). */
+int mxh_device_info(mxh_gpu *g, int *cus, int *clock_khz);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MAXIM_HIP_H */

@@ -1,0 +1,944 @@
+// The gfx950 executor: one plan, one device arena, one stream.
+//
+// The per-op dispatch follows the reference's `Gpu::op` (src/exec_gpu.rs
+// 359-739) in what it computes; the kernels, their launch geometry and the
+// device weight layouts are this engine's own. Everything that can be decided
+// before the first launch is: `Gpu::Gpu` validates every op against the
+// buffer table (so no kernel is ever launched over a shape it was not written
+// for), converts each weight to the layout its kernel reads, builds the resize
+// tap tables, uploads all of it in one copy, and records every launch (kernel,
+// grid, argument block) so that running the plan is a loop of launches.
+
+#include <algorithm>
+#include <array>
+#include <cmath>
+#include <cstdlib>
+#include <cstring>
+#include <map>
+#include <memory>
+#include <set>
+#include <string>
+#include <vector>
+
+#include "../hip/kargs.h"
+#include "hip_api.hpp"
+#include "host.hpp"
+#include "maxim_hip.h"
+
+extern "C" const unsigned char mx_kernels_hsaco[];
+extern "C" const unsigned char mx_kernels_hsaco_end[];
+
+namespace mxh {
+
+using mx::Error;
+
+namespace {
+
+struct Launch {
+    hipFunction_t f = nullptr;
+    const char *name = "";
+    unsigned g[3] = {1, 1, 1};
+    unsigned b[3] = {MXK_BLOCK, 1, 1};
+    alignas(16) unsigned char a0[128];
+    alignas(16) unsigned char a1[32];
+    int nparams = 1;
+};
+
+template <typename T>
+void set_args(Launch &l, const T &v) {
+    static_assert(sizeof(T) <= sizeof(l.a0), "argument block too large");
+    memcpy(l.a0, &v, sizeof(T));
+    l.nparams = 1;
+}
+
+template <typename T, typename U>
+void set_args(Launch &l, const T &v, const U &w) {
+    static_assert(sizeof(T) <= sizeof(l.a0) && sizeof(U) <= sizeof(l.a1), "argument block too large");
+    memcpy(l.a0, &v, sizeof(T));
+    memcpy(l.a1, &w, sizeof(U));
+    l.nparams = 2;
+}
+
+unsigned cdiv(int64_t a, int64_t b) {
+    int64_t q = (a + b - 1) / b;
+    if (q < 1) q = 1;
+    if (q > 0x7fffffff) throw Error("a launch needs more than 2^31 blocks");
+    return (unsigned)q;
+}
+
+unsigned grid_yz(int64_t n) {
+    if (n < 1) n = 1;
+    if (n > 65535) throw Error("a launch needs more than 65535 blocks on a y/z grid axis");
+    return (unsigned)n;
+}
+
+bool aligned(const void *p, size_t a) { return ((uintptr_t)p % a) == 0; }
+
+// The resize tap table of one axis: per output [j0, n, wsum, w0 .. w(maxt-1)],
+// built with the CPU path's arithmetic (src/exec_cpu.rs:1195-1216) in fp32,
+// so the device sums the same weights in the same order.
+std::vector<float> resize_table(int64_t n_in, int64_t n_out, int &maxt) {
+    const float inv = (float)n_in / (float)n_out;
+    const float kscale = inv > 1.0f ? inv : 1.0f;
+    std::vector<std::vector<float>> taps(n_out);
+    std::vector<int64_t> j0s(n_out);
+    std::vector<float> sums(n_out);
+    maxt = 1;
+    for (int64_t o = 0; o < n_out; ++o) {
+        const float sample = ((float)o + 0.5f) * inv - 0.5f;
+        int64_t j0 = (int64_t)std::ceil(sample - kscale);
+        int64_t j1 = (int64_t)std::floor(sample + kscale);
+        if (j0 < 0) j0 = 0;
+        if (j1 > n_in - 1) j1 = n_in - 1;
+        float s = 0.0f;
+        for (int64_t j = j0; j <= j1; ++j) {
+            float d = std::fabs(sample - (float)j) / kscale;
+            if (d < 1.0f) {
+                float wv = 1.0f - d;
+                taps[o].push_back(wv);
+                s += wv;
+            }
+        }
+        // The CPU applies the k-th kept weight to input j0 + k; a table whose
+        // run would read past the row is refused rather than clamped.
+        if (j0 + (int64_t)taps[o].size() > n_in) throw Error("resize: a tap run leaves the input row");
+        j0s[o] = j0;
+        sums[o] = s;
+        maxt = std::max<int>(maxt, (int)taps[o].size());
+    }
+    std::vector<float> t((size_t)n_out * (3 + maxt), 0.0f);
+    for (int64_t o = 0; o < n_out; ++o) {
+        float *e = &t[(size_t)o * (3 + maxt)];
+        e[0] = (float)j0s[o];
+        e[1] = (float)taps[o].size();
+        e[2] = sums[o];
+        for (size_t k = 0; k < taps[o].size(); ++k) e[3 + k] = taps[o][k];
+    }
+    return t;
+}
+
+struct ResizeTab {
+    const float *t;
+    int32_t maxt, pad;
+};
+
+}  // namespace
+
+class Gpu {
+public:
+    explicit Gpu(const mx_plan_desc *p);
+    ~Gpu();
+
+    HipApi &H;
+    hipModule_t mod = nullptr;
+    hipStream_t stream = nullptr;
+    float *arena = nullptr;
+    uint64_t arena_len = 0;
+    unsigned char *wdev = nullptr;
+    uint64_t wbytes = 0;
+    float *scratch = nullptr;
+    uint64_t scratch_len = 0;
+    uint64_t n_ops = 0, n_bufs = 0;
+    std::vector<std::vector<Launch>> ops;
+    uint64_t launched = 0, kernels = 0;
+    bool want_timeline = false;
+    std::vector<float> per_op_ms;
+    float total_ms = 0.0f;
+    bool have_timeline = false;
+    std::string name;
+    int cus = 0, clock_khz = 0;
+
+    void check_plan(const mx_plan_desc *p) const {
+        if (p->n_ops != n_ops || p->n_bufs != n_bufs || p->arena_len != arena_len)
+            throw Error("this executor was built for a different plan");
+    }
+    void launch(Launch &l) {
+        void *params[2] = {l.a0, l.a1};
+        check(H.hipModuleLaunchKernel(l.f, l.g[0], l.g[1], l.g[2], l.b[0], l.b[1], l.b[2], 0, stream,
+                                      params, nullptr),
+              l.name);
+        ++kernels;
+    }
+    void run_op(uint64_t i) {
+        for (auto &l : ops[i]) launch(l);
+        ++launched;
+    }
+    void sync() { check(H.hipStreamSynchronize(stream), "hipStreamSynchronize"); }
+    // All ops with an event before each and one after the last; one sync.
+    void run_timed(uint64_t n) {
+        std::vector<hipEvent_t> ev(n + 1);
+        for (auto &e : ev) check(H.hipEventCreate(&e), "hipEventCreate");
+        for (uint64_t i = 0; i < n; ++i) {
+            check(H.hipEventRecord(ev[i], stream), "hipEventRecord");
+            run_op(i);
+        }
+        check(H.hipEventRecord(ev[n], stream), "hipEventRecord");
+        sync();
+        per_op_ms.assign(n, 0.0f);
+        total_ms = 0.0f;
+        for (uint64_t i = 0; i < n; ++i) {
+            check(H.hipEventElapsedTime(&per_op_ms[i], ev[i], ev[i + 1]), "hipEventElapsedTime");
+            total_ms += per_op_ms[i];
+        }
+        for (auto &e : ev) H.hipEventDestroy(e);
+        have_timeline = true;
+    }
+    void write(uint64_t off, const float *v, uint64_t n) {
+        if (n == 0) return;
+        if (off + n > arena_len) throw Error("a write of " + std::to_string(n) + " floats at " + std::to_string(off) + " runs past the arena");
+        check(H.hipMemcpyAsync(arena + off, v, n * 4, kMemcpyH2D, stream), "hipMemcpyAsync(H2D)");
+        sync();
+    }
+    void read(uint64_t off, float *v, uint64_t n) {
+        if (n == 0) return;
+        if (off + n > arena_len) throw Error("a read of " + std::to_string(n) + " floats at " + std::to_string(off) + " runs past the arena");
+        check(H.hipMemcpyAsync(v, arena + off, n * 4, kMemcpyD2H, stream), "hipMemcpyAsync(D2H)");
+        sync();
+    }
+
+private:
+    std::map<std::string, hipFunction_t> fns_;
+    std::set<std::string> names_;
+    const char *intern(const std::string &s) { return names_.insert(s).first->c_str(); }
+    hipFunction_t fn(const char *name) {
+        auto it = fns_.find(name);
+        if (it != fns_.end()) return it->second;
+        hipFunction_t f = nullptr;
+        check(H.hipModuleGetFunction(&f, mod, name), (std::string("hipModuleGetFunction ") + name).c_str());
+        fns_[name] = f;
+        return f;
+    }
+    Launch mk(const std::string &kname) {
+        Launch l;
+        l.name = intern(kname);
+        l.f = fn(l.name);
+        return l;
+    }
+    void validate(const mx_plan_desc *p) const;
+    void build_launches(const mx_plan_desc *p, const std::vector<int64_t> &woff,
+                        const std::vector<std::array<int64_t, 4>> &extra,
+                        const std::vector<std::array<int, 2>> &maxt);
+};
+
+// Every op is checked against the buffer table before anything touches the
+// device: a wrong dimension would otherwise become an out-of-bounds kernel.
+void Gpu::validate(const mx_plan_desc *p) const {
+    auto len = [&](int64_t id) -> uint64_t {
+        if (id < 0 || (uint64_t)id >= p->n_bufs) throw Error("an op names buffer " + std::to_string(id) + ", which does not exist");
+        const mx_bufshape &s = p->bufs[id];
+        uint64_t n = (uint64_t)(s.c * s.h * s.w);
+        if (p->offs[id] + n > p->arena_len) throw Error("buffer " + std::to_string(id) + " runs past the arena");
+        return n;
+    };
+    auto wlen = [&](int64_t id) -> uint64_t {
+        if (id < 0 || (uint64_t)id >= p->n_weights) throw Error("an op names weight " + std::to_string(id) + ", which does not exist");
+        return p->weight_lens[id];
+    };
+    auto shape = [&](int64_t id, int64_t c, int64_t h, int64_t w, const char *what) {
+        const mx_bufshape &s = p->bufs[id];
+        len(id);
+        if (s.c != c || s.h != h || s.w != w)
+            throw Error(std::string(what) + ": buffer " + std::to_string(id) + " is not [" + std::to_string(c) + "][" +
+                        std::to_string(h) + "][" + std::to_string(w) + "]");
+    };
+    auto need = [](bool ok, const char *what) {
+        if (!ok) throw Error(std::string("inconsistent op: ") + what);
+    };
+    for (uint64_t i = 0; i < p->n_ops; ++i) {
+        const mx_op &o = p->ops[i];
+        try {
+            switch (o.kind) {
+                case MX_OP_COPY:
+                case MX_OP_GELU:
+                case MX_OP_LRELU:
+                case MX_OP_SIGMOID:
+                    need(o.n >= 0 && (uint64_t)o.n <= len(o.dst) && (uint64_t)o.n <= len(o.src), "elementwise n");
+                    break;
+                case MX_OP_ADD:
+                case MX_OP_MUL:
+                case MX_OP_GATE_APPLY:
+                    need((uint64_t)o.n == len(o.dst) && (uint64_t)o.n == len(o.src) && (uint64_t)o.n == len(o.src2), "binary n");
+                    break;
+                case MX_OP_CHAN_LN:
+                    need(len(o.dst) == (uint64_t)(o.c * o.hw) && len(o.src) == (uint64_t)(o.c * o.hw), "chan_ln shape");
+                    need(wlen(o.scale) == (uint64_t)o.c && wlen(o.bias) == (uint64_t)o.c, "chan_ln weights");
+                    break;
+                case MX_OP_CHAN_MEAN:
+                    need(len(o.dst) == (uint64_t)o.c && len(o.src) == (uint64_t)(o.c * o.hw) && o.hw > 0, "chan_mean shape");
+                    break;
+                case MX_OP_CHAN_SCALE:
+                    need(len(o.src2) == (uint64_t)o.c && len(o.dst) >= (uint64_t)(o.c * o.hw) && len(o.src) >= (uint64_t)(o.c * o.hw), "chan_scale shape");
+                    break;
+                case MX_OP_CONV1X1:
+                    shape(o.dst, o.c_out, o.h, o.wd, "conv1x1 out");
+                    shape(o.src, o.c_in, o.h, o.wd, "conv1x1 in");
+                    need(wlen(o.w) == (uint64_t)(o.c_in * o.c_out), "conv1x1 weight");
+                    if (o.bias >= 0) need(wlen(o.bias) == (uint64_t)o.c_out, "conv1x1 bias");
+                    break;
+                case MX_OP_CONV3X3:
+                    shape(o.dst, o.c_out, o.h, o.wd, "conv3x3 out");
+                    shape(o.src, o.c_in, o.h, o.wd, "conv3x3 in");
+                    need(wlen(o.w) == (uint64_t)(9 * o.c_in * o.c_out), "conv3x3 weight");
+                    if (o.bias >= 0) need(wlen(o.bias) == (uint64_t)o.c_out, "conv3x3 bias");
+                    break;
+                case MX_OP_CONV4X4S2:
+                    shape(o.dst, o.c_out, o.oh, o.ow, "conv4x4 out");
+                    shape(o.src, o.c_in, o.h, o.wd, "conv4x4 in");
+                    need(wlen(o.w) == (uint64_t)(16 * o.c_in * o.c_out), "conv4x4 weight");
+                    if (o.bias >= 0) need(wlen(o.bias) == (uint64_t)o.c_out, "conv4x4 bias");
+                    need(o.p[0] >= 0 && o.p[0] < 4 && o.p[1] >= 0 && o.p[1] < 4, "conv4x4 padding");
+                    break;
+                case MX_OP_CONVT2X2:
+                    shape(o.dst, o.c_out, 2 * o.h, 2 * o.wd, "convt out");
+                    shape(o.src, o.c_in, o.h, o.wd, "convt in");
+                    need(wlen(o.w) == (uint64_t)(4 * o.c_in * o.c_out), "convt weight");
+                    if (o.bias >= 0) need(wlen(o.bias) == (uint64_t)o.c_out, "convt bias");
+                    break;
+                case MX_OP_GATE_MM: {
+                    int64_t outer = o.p[0], inner = o.p[1], k = o.mode == 0 ? outer : inner;
+                    shape(o.dst, o.c, outer, inner, "gate_mm out");
+                    shape(o.src, o.c, outer, inner, "gate_mm in");
+                    need(o.mode == 0 || o.mode == 1, "gate_mm mode");
+                    need(wlen(o.w) == (uint64_t)(k * k), "gate_mm weight");
+                    if (o.bias >= 0) need(wlen(o.bias) == (uint64_t)k, "gate_mm bias");
+                    break;
+                }
+                case MX_OP_BLOCK_PERM: {
+                    int64_t gh = o.p[0], gw = o.p[1], fh = o.p[2], fw = o.p[3];
+                    need(gh > 0 && gw > 0 && fh > 0 && fw > 0 && gh * fh <= o.h && gw * fw <= o.wd, "block_perm cells");
+                    need(len(o.src) >= (uint64_t)(o.c * o.h * o.wd) && len(o.dst) >= (uint64_t)(o.c * o.h * o.wd), "block_perm size");
+                    need(len(o.src) == len(o.dst), "block_perm sizes differ");
+                    break;
+                }
+                case MX_OP_RESIZE:
+                    shape(o.dst, o.c, o.oh, o.ow, "resize out");
+                    shape(o.src, o.c, o.h, o.wd, "resize in");
+                    shape(o.src2, o.c, o.h, o.ow, "resize tmp");
+                    break;
+                case MX_OP_DOWN_S:
+                    shape(o.dst, o.c, o.oh, o.ow, "down out");
+                    shape(o.src, o.c, o.h, o.wd, "down in");
+                    need((o.oh - 1) * o.p[0] + o.p[1] < o.h && (o.ow - 1) * o.p[0] + o.p[1] < o.wd, "down range");
+                    break;
+                default:
+                    throw Error("unknown op kind " + std::to_string(o.kind));
+            }
+        } catch (const Error &e) {
+            throw Error("op " + std::to_string(i) + ": " + e.what());
+        }
+    }
+}
+
+Gpu::Gpu(const mx_plan_desc *p) : H(hip()) {
+    validate(p);
+    check(H.hipInit(0), "hipInit");
+    int ndev = 0;
+    check(H.hipGetDeviceCount(&ndev), "hipGetDeviceCount");
+    if (ndev < 1) throw Error("no HIP device");
+    check(H.hipSetDevice(0), "hipSetDevice");
+    char nm[256] = {0};
+    if (H.hipDeviceGetName(nm, sizeof nm - 1, 0) == 0) name = nm;
+    H.hipDeviceGetAttribute(&cus, kAttrMultiprocessorCount, 0);
+    H.hipDeviceGetAttribute(&clock_khz, kAttrClockRate, 0);
+    check(H.hipModuleLoadData(&mod, mx_kernels_hsaco), "hipModuleLoadData (embedded gfx950 code object)");
+    check(H.hipStreamCreate(&stream), "hipStreamCreate");
+
+    // Device weights, in the layout each kernel reads, packed into one blob.
+    std::vector<float> blob;
+    auto place = [&](const float *v, uint64_t n) -> int64_t {
+        blob.resize((blob.size() + 63) & ~(size_t)63);
+        int64_t off = (int64_t)blob.size();
+        blob.insert(blob.end(), v, v + n);
+        return off;
+    };
+    auto placev = [&](const std::vector<float> &v) { return place(v.data(), v.size()); };
+    const size_t nw = p->n_weights;
+    std::vector<int64_t> woff(nw, -1);
+    auto as_is = [&](int64_t id) {
+        if (id >= 0 && woff[id] < 0) woff[id] = place(p->weights[id], p->weight_lens[id]);
+    };
+    std::vector<std::array<int64_t, 4>> extra(p->n_ops, {-1, -1, -1, -1});  // per-op derived blobs
+    std::vector<std::array<int, 2>> maxt(p->n_ops, {0, 0});
+    uint64_t mean_scratch = 0;
+    for (uint64_t i = 0; i < p->n_ops; ++i) {
+        const mx_op &o = p->ops[i];
+        switch (o.kind) {
+            case MX_OP_CHAN_LN:
+                as_is(o.scale);
+                as_is(o.bias);
+                break;
+            case MX_OP_CHAN_MEAN: {
+                int64_t chunk = std::max<int64_t>(2048, ((o.hw + 63) / 64 + 255) / 256 * 256);
+                int64_t nchunk = (o.hw + chunk - 1) / chunk;
+                mean_scratch = std::max<uint64_t>(mean_scratch, (uint64_t)(o.c * nchunk));
+                break;
+            }
+            case MX_OP_CONV1X1:
+                as_is(o.w);
+                as_is(o.bias);
+                break;
+            case MX_OP_CONV3X3:
+            case MX_OP_CONV4X4S2: {
+                // [co][ci][k][k] -> [co][tap][ci]
+                const int taps = o.kind == MX_OP_CONV3X3 ? 9 : 16;
+                const float *w = p->weights[o.w];
+                std::vector<float> t((size_t)(o.c_out * o.c_in * taps));
+                for (int64_t m = 0; m < o.c_out; ++m)
+                    for (int64_t c = 0; c < o.c_in; ++c)
+                        for (int tp = 0; tp < taps; ++tp)
+                            t[(m * taps + tp) * o.c_in + c] = w[(m * o.c_in + c) * taps + tp];
+                extra[i][0] = placev(t);
+                as_is(o.bias);
+                break;
+            }
+            case MX_OP_CONVT2X2: {
+                // [ci][co][2][2] (flipped) -> [tap][co][ci]
+                const float *w = p->weights[o.w];
+                std::vector<float> t((size_t)(4 * o.c_out * o.c_in));
+                for (int64_t c = 0; c < o.c_in; ++c)
+                    for (int64_t m = 0; m < o.c_out; ++m)
+                        for (int tp = 0; tp < 4; ++tp) t[(tp * o.c_out + m) * o.c_in + c] = w[(c * o.c_out + m) * 4 + tp];
+                extra[i][0] = placev(t);
+                as_is(o.bias);
+                break;
+            }
+            case MX_OP_GATE_MM: {
+                if (o.mode == 0) {
+                    as_is(o.w);
+                } else {
+                    // [a][t] -> [t][a], the B operand of X . W^T
+                    const int64_t k = o.p[1];
+                    const float *w = p->weights[o.w];
+                    std::vector<float> t((size_t)(k * k));
+                    for (int64_t a = 0; a < k; ++a)
+                        for (int64_t tt = 0; tt < k; ++tt) t[tt * k + a] = w[a * k + tt];
+                    extra[i][0] = placev(t);
+                }
+                as_is(o.bias);
+                break;
+            }
+            case MX_OP_RESIZE: {
+                extra[i][0] = placev(resize_table(o.wd, o.ow, maxt[i][0]));
+                extra[i][1] = placev(resize_table(o.h, o.oh, maxt[i][1]));
+                break;
+            }
+            default:
+                break;
+        }
+    }
+    blob.resize((blob.size() + 63) & ~(size_t)63);
+
+    // Size the pass before allocating it, and refuse with the numbers.
+    arena_len = p->arena_len;
+    n_ops = p->n_ops;
+    n_bufs = p->n_bufs;
+    wbytes = blob.size() * 4;
+    scratch_len = std::max<uint64_t>(mean_scratch, 64);
+    const uint64_t need = arena_len * 4 + wbytes + scratch_len * 4;
+    size_t free_b = 0, total_b = 0;
+    if (H.hipMemGetInfo(&free_b, &total_b) == 0 && need > free_b) {
+        throw Error("not enough device memory for a " + std::to_string(p->bufs[p->input].w) + "x" +
+                    std::to_string(p->bufs[p->input].h) + " pass\nmaxim: the arena needs " +
+                    std::to_string((arena_len * 4) >> 20) + " MiB and the weights " + std::to_string(wbytes >> 20) +
+                    " MiB; " + std::to_string(free_b >> 20) +
+                    " MiB is free\nmaxim: the arena is exact - it is the plan's own packed size - so this is a hard limit");
+    }
+    void *ptr = nullptr;
+    hipError_t rc = H.hipMalloc(&ptr, std::max<uint64_t>(arena_len, 1) * 4);
+    if (rc != 0)
+        throw Error("the arena (" + std::to_string((arena_len * 4) >> 20) + " MiB) did not fit after all, with " +
+                    std::to_string(free_b >> 20) + " MiB free: " + H.hipGetErrorString(rc));
+    arena = static_cast<float *>(ptr);
+    check(H.hipMalloc(&ptr, std::max<uint64_t>(wbytes, 256)), "hipMalloc(weights)");
+    wdev = static_cast<unsigned char *>(ptr);
+    check(H.hipMalloc(&ptr, scratch_len * 4), "hipMalloc(scratch)");
+    scratch = static_cast<float *>(ptr);
+    if (wbytes) check(H.hipMemcpy(wdev, blob.data(), wbytes, kMemcpyH2D), "hipMemcpy(weights)");
+
+    build_launches(p, woff, extra, maxt);
+}
+
+void Gpu::build_launches(const mx_plan_desc *p, const std::vector<int64_t> &woff,
+                         const std::vector<std::array<int64_t, 4>> &extra,
+                         const std::vector<std::array<int, 2>> &maxt) {
+    auto B = [&](int64_t id) { return arena + p->offs[id]; };
+    auto W = [&](int64_t id) -> const float * {
+        return id >= 0 ? reinterpret_cast<const float *>(wdev) + woff[id] : nullptr;
+    };
+    auto X = [&](uint64_t i, int k) { return reinterpret_cast<const float *>(wdev) + extra[i][k]; };
+    ops.assign(p->n_ops, {});
+    for (uint64_t i = 0; i < p->n_ops; ++i) {
+        const mx_op &o = p->ops[i];
+        auto &L = ops[i];
+        switch (o.kind) {
+            case MX_OP_COPY:
+            case MX_OP_ADD:
+            case MX_OP_MUL:
+            case MX_OP_GATE_APPLY:
+            case MX_OP_GELU:
+            case MX_OP_LRELU:
+            case MX_OP_SIGMOID: {
+                if (o.n == 0) break;
+                static const char *v4[] = {"mx_copy_v4", "mx_add_v4", "mx_mul_v4", "mx_gate_apply_v4",
+                                           "mx_gelu_v4", "mx_lrelu_v4", "mx_sigmoid_v4"};
+                static const char *s1[] = {"mx_copy_s", "mx_add_s", "mx_mul_s", "mx_gate_apply_s",
+                                           "mx_gelu_s", "mx_lrelu_s", "mx_sigmoid_s"};
+                int k;
+                switch (o.kind) {
+                    case MX_OP_COPY: k = MXK_COPY; break;
+                    case MX_OP_ADD: k = MXK_ADD; break;
+                    case MX_OP_MUL: k = MXK_MUL; break;
+                    case MX_OP_GATE_APPLY: k = MXK_GATE_APPLY; break;
+                    case MX_OP_GELU: k = MXK_GELU; break;
+                    case MX_OP_LRELU: k = MXK_LRELU; break;
+                    default: k = MXK_SIGMOID; break;
+                }
+                EwArgs a{};
+                a.a = B(o.src);
+                a.b = o.src2 >= 0 ? B(o.src2) : nullptr;
+                a.y = B(o.dst);
+                a.n = o.n;
+                a.op = k;
+                a.slope = o.slope;
+                bool vec = o.n % 4 == 0 && aligned(a.a, 16) && aligned(a.y, 16) && (!a.b || aligned(a.b, 16));
+                Launch l = mk(vec ? v4[k] : s1[k]);
+                l.g[0] = vec ? cdiv(o.n / 4, MXK_BLOCK * 4) : cdiv(o.n, MXK_BLOCK);
+                set_args(l, a);
+                L.push_back(l);
+                break;
+            }
+            case MX_OP_CHAN_SCALE: {
+                ChanScaleArgs a{B(o.src), B(o.src2), B(o.dst), o.hw, o.c};
+                bool vec = o.hw % 4 == 0 && aligned(a.x, 16) && aligned(a.y, 16);
+                Launch l = mk(vec ? "mx_chan_scale_v4" : "mx_chan_scale_s");
+                l.g[0] = vec ? cdiv(o.hw / 4, MXK_BLOCK * 4) : cdiv(o.hw, MXK_BLOCK);
+                l.g[1] = grid_yz(o.c);
+                set_args(l, a);
+                L.push_back(l);
+                break;
+            }
+            case MX_OP_CHAN_LN: {
+                ChanLnArgs a{B(o.src), W(o.scale), W(o.bias), B(o.dst), o.hw, (int32_t)o.c, mx::kEps};
+                const char *k = "mx_chan_ln_any";
+                int v = 1;
+                if (o.c == 32 && o.hw % 4 == 0 && aligned(a.x, 16) && aligned(a.y, 16)) { k = "mx_chan_ln_c32"; v = 4; }
+                else if (o.c == 64 && o.hw % 2 == 0 && aligned(a.x, 8) && aligned(a.y, 8)) { k = "mx_chan_ln_c64"; v = 2; }
+                else if (o.c == 128) { k = "mx_chan_ln_c128"; v = 1; }
+                Launch l = mk(k);
+                l.g[0] = cdiv(o.hw / v, MXK_BLOCK);
+                set_args(l, a);
+                L.push_back(l);
+                break;
+            }
+            case MX_OP_CHAN_MEAN: {
+                int64_t chunk = std::max<int64_t>(2048, ((o.hw + 63) / 64 + 255) / 256 * 256);
+                int32_t nchunk = (int32_t)((o.hw + chunk - 1) / chunk);
+                ChanMeanArgs a{B(o.src), scratch, B(o.dst), o.hw, chunk, (int32_t)o.c, nchunk};
+                Launch l1 = mk("mx_chan_mean_part");
+                l1.g[0] = (unsigned)nchunk;
+                l1.g[1] = grid_yz(o.c);
+                set_args(l1, a);
+                L.push_back(l1);
+                Launch l2 = mk("mx_chan_mean_final");
+                l2.g[0] = cdiv(o.c, MXK_BLOCK);
+                set_args(l2, a);
+                L.push_back(l2);
+                break;
+            }
+            case MX_OP_CONV1X1: {
+                const int64_t plane = o.h * o.wd;
+                if (plane == 1) {
+                    GemvArgs a{W(o.w), B(o.src), W(o.bias), B(o.dst), (int32_t)o.c_in, (int32_t)o.c_out};
+                    Launch l = mk("mx_gemv");
+                    l.g[0] = cdiv(o.c_out, MXK_BLOCK);
+                    set_args(l, a);
+                    L.push_back(l);
+                    break;
+                }
+                GemmArgs a{};
+                a.A = W(o.w);
+                a.B = B(o.src);
+                a.bias = W(o.bias);
+                a.C = B(o.dst);
+                a.M = (int32_t)o.c_out;
+                a.N = (int32_t)plane;
+                a.K = (int32_t)o.c_in;
+                a.batch = 1;
+                a.bias_mode = o.bias >= 0 ? MXK_BIAS_ROW : MXK_BIAS_NONE;
+                a.epi = MXK_EPI_PLAIN;
+                if (plane > 0x7fffffff) throw Error("conv1x1 plane too large");
+                bool vec = plane % 4 == 0 && aligned(a.B, 16);
+                int bm = o.c_out <= 32 ? 32 : o.c_out <= 64 ? 64 : 128;
+                const char *k = bm == 32 ? (vec ? "mx_gemm_32x128_v4" : "mx_gemm_32x128")
+                                : bm == 64 ? (vec ? "mx_gemm_64x128_v4" : "mx_gemm_64x128")
+                                           : (vec ? "mx_gemm_128x128_v4" : "mx_gemm_128x128");
+                Launch l = mk(k);
+                l.g[0] = cdiv(plane, 128);
+                l.g[1] = grid_yz((o.c_out + bm - 1) / bm);
+                set_args(l, a);
+                L.push_back(l);
+                break;
+            }
+            case MX_OP_CONV3X3:
+            case MX_OP_CONV4X4S2: {
+                const bool k3 = o.kind == MX_OP_CONV3X3;
+                ConvArgs a{};
+                a.x = B(o.src);
+                a.w = X(i, 0);
+                a.bias = W(o.bias);
+                a.y = B(o.dst);
+                a.ci = (int32_t)o.c_in;
+                a.co = (int32_t)o.c_out;
+                a.h = (int32_t)o.h;
+                a.wd = (int32_t)o.wd;
+                a.oh = (int32_t)(k3 ? o.h : o.oh);
+                a.ow = (int32_t)(k3 ? o.wd : o.ow);
+                a.pad_top = (int32_t)(k3 ? 1 : o.p[0]);
+                a.pad_left = (int32_t)(k3 ? 1 : o.p[1]);
+                int bm = o.c_out <= 32 ? 32 : o.c_out <= 64 ? 64 : 128;
+                std::string k = std::string(k3 ? "mx_conv3x3_m" : "mx_conv4x4_m") + std::to_string(bm);
+                if (k3 && o.c_in <= 4) k += "_c4";
+                Launch l = mk(k);
+                const int64_t tiles = (int64_t)((a.oh + 7) / 8) * ((a.ow + 15) / 16);
+                l.g[0] = cdiv(tiles, 1);
+                l.g[1] = grid_yz((o.c_out + bm - 1) / bm);
+                set_args(l, a);
+                L.push_back(l);
+                break;
+            }
+            case MX_OP_CONVT2X2: {
+                const int64_t plane = o.h * o.wd;
+                GemmArgs a{};
+                a.A = X(i, 0);
+                a.B = B(o.src);
+                a.bias = W(o.bias);
+                a.C = B(o.dst);
+                a.M = (int32_t)(4 * o.c_out);
+                a.N = (int32_t)plane;
+                a.K = (int32_t)o.c_in;
+                a.batch = 1;
+                a.bias_mode = MXK_BIAS_NONE;
+                a.epi = MXK_EPI_CONVT;
+                a.co = (int32_t)o.c_out;
+                a.wd = (int32_t)o.wd;
+                bool vec = plane % 4 == 0 && aligned(a.B, 16);
+                Launch l = mk(vec ? "mx_gemm_128x128_v4" : "mx_gemm_128x128");
+                l.g[0] = cdiv(plane, 128);
+                l.g[1] = grid_yz((a.M + 127) / 128);
+                set_args(l, a);
+                L.push_back(l);
+                break;
+            }
+            case MX_OP_GATE_MM: {
+                const int64_t outer = o.p[0], inner = o.p[1];
+                GemmArgs a{};
+                a.bias = W(o.bias);
+                a.C = B(o.dst);
+                a.epi = MXK_EPI_PLAIN;
+                if (o.mode == 0) {
+                    // per channel: Y[c] = W . X[c], bias by row
+                    a.A = W(o.w);
+                    a.B = B(o.src);
+                    a.sA = 0;
+                    a.sB = a.sC = outer * inner;
+                    a.M = (int32_t)outer;
+                    a.K = (int32_t)outer;
+                    a.N = (int32_t)inner;
+                    a.batch = (int32_t)o.c;
+                    a.bias_mode = o.bias >= 0 ? MXK_BIAS_ROW : MXK_BIAS_NONE;
+                    bool vec = inner % 4 == 0 && aligned(a.B, 16);
+                    int bm = outer <= 64 ? 64 : 128;
+                    const char *k = bm == 64 ? (vec ? "mx_gemm_64x128_v4" : "mx_gemm_64x128")
+                                             : (vec ? "mx_gemm_128x128_v4" : "mx_gemm_128x128");
+                    Launch l = mk(k);
+                    l.g[0] = cdiv(inner, 128);
+                    l.g[1] = grid_yz((outer + bm - 1) / bm);
+                    l.g[2] = grid_yz(o.c);
+                    set_args(l, a);
+                    L.push_back(l);
+                } else {
+                    // all channels at once: Y = X . W^T, bias by column
+                    a.A = B(o.src);
+                    a.B = X(i, 0);
+                    a.M = (int32_t)(o.c * outer);
+                    a.K = (int32_t)inner;
+                    a.N = (int32_t)inner;
+                    a.batch = 1;
+                    a.bias_mode = o.bias >= 0 ? MXK_BIAS_COL : MXK_BIAS_NONE;
+                    if (o.c * outer > 0x7fffffff) throw Error("gate_mm rows too many");
+                    bool wide = inner > 64;
+                    const char *k = wide ? "mx_gemm_128x128_v4" : "mx_gemm_128x64_v4";
+                    if (inner % 4 != 0) k = wide ? "mx_gemm_128x128" : "mx_gemm_128x64";
+                    Launch l = mk(k);
+                    l.g[0] = cdiv(inner, wide ? 128 : 64);
+                    l.g[1] = grid_yz((a.M + 127) / 128);
+                    set_args(l, a);
+                    L.push_back(l);
+                }
+                break;
+            }
+            case MX_OP_BLOCK_PERM: {
+                PermArgs a{};
+                a.x = B(o.src);
+                a.y = B(o.dst);
+                a.c = o.c;
+                a.h = (int32_t)o.h;
+                a.wd = (int32_t)o.wd;
+                a.gh = (int32_t)o.p[0];
+                a.gw = (int32_t)o.p[1];
+                a.fh = (int32_t)o.p[2];
+                a.fw = (int32_t)o.p[3];
+                a.swap = (o.mode & MX_PERM_SWAP) ? 1 : 0;
+                a.forward = (o.mode & MX_PERM_FORWARD) ? 1 : 0;
+                int v = 1;
+                if (!a.swap && a.fw % 4 == 0 && a.wd % 4 == 0 && aligned(a.x, 16) && aligned(a.y, 16)) v = 4;
+                else if (!a.swap && a.fw % 2 == 0 && a.wd % 2 == 0 && aligned(a.x, 8) && aligned(a.y, 8)) v = 2;
+                Launch l = mk(v == 4 ? "mx_block_perm_v4" : v == 2 ? "mx_block_perm_v2" : "mx_block_perm_v1");
+                const int64_t psz = o.p[2] * o.p[3];
+                l.g[0] = cdiv(o.c * o.p[0] * o.p[1], 1);
+                l.b[0] = psz / v <= 64 ? 64 : psz / v <= 128 ? 128 : MXK_BLOCK;
+                set_args(l, a);
+                L.push_back(l);
+                break;
+            }
+            case MX_OP_RESIZE: {
+                ResizeArgs h{};
+                h.x = B(o.src);
+                h.y = B(o.src2);
+                h.rows = o.c * o.h;
+                h.n_in = (int32_t)o.wd;
+                h.n_out = (int32_t)o.ow;
+                h.width = 1;
+                h.axis = 2;
+                ResizeTab th{X(i, 0), maxt[i][0], 0};
+                Launch l1 = mk("mx_resize_h");
+                l1.g[0] = cdiv(h.rows * o.ow, MXK_BLOCK);
+                set_args(l1, h, th);
+                L.push_back(l1);
+                ResizeArgs v{};
+                v.x = B(o.src2);
+                v.y = B(o.dst);
+                v.rows = o.c;
+                v.n_in = (int32_t)o.h;
+                v.n_out = (int32_t)o.oh;
+                v.width = (int32_t)o.ow;
+                v.axis = 1;
+                ResizeTab tv{X(i, 1), maxt[i][1], 0};
+                Launch l2 = mk("mx_resize_v");
+                l2.g[0] = cdiv(o.c * o.oh * o.ow, MXK_BLOCK);
+                set_args(l2, v, tv);
+                L.push_back(l2);
+                break;
+            }
+            case MX_OP_DOWN_S: {
+                DownArgs a{B(o.src), B(o.dst), o.c, (int32_t)o.h, (int32_t)o.wd, (int32_t)o.p[0],
+                           (int32_t)o.p[1], (int32_t)o.oh, (int32_t)o.ow};
+                Launch l = mk("mx_down_s");
+                l.g[0] = cdiv(o.c * o.oh * o.ow, MXK_BLOCK);
+                set_args(l, a);
+                L.push_back(l);
+                break;
+            }
+            default:
+                throw Error("op " + std::to_string(i) + ": no kernel for kind " + std::to_string(o.kind));
+        }
+    }
+}
+
+Gpu::~Gpu() {
+    if (stream) H.hipStreamSynchronize(stream);
+    if (arena) H.hipFree(arena);
+    if (wdev) H.hipFree(wdev);
+    if (scratch) H.hipFree(scratch);
+    if (stream) H.hipStreamDestroy(stream);
+    if (mod) H.hipModuleUnload(mod);
+}
+
+}  // namespace mxh
+
+using mxh::Gpu;
+
+namespace {
+
+template <typename F>
+int guard(F &&f) {
+    try {
+        f();
+        return 0;
+    } catch (const std::exception &e) {
+        mx::set_error(e.what());
+        return -1;
+    }
+}
+
+Gpu *G(mxh_gpu *g) { return reinterpret_cast<Gpu *>(g); }
+
+}  // namespace
+
+extern "C" {
+
+int mxh_driver_ready(void) {
+    return guard([] {
+        auto &H = mxh::hip();
+        mxh::check(H.hipInit(0), "hipInit");
+        int n = 0;
+        mxh::check(H.hipGetDeviceCount(&n), "hipGetDeviceCount");
+        if (n < 1) throw mx::Error("no HIP device");
+    });
+}
+
+mxh_gpu *mxh_new(const mx_plan_desc *plan) {
+    Gpu *g = nullptr;
+    guard([&] {
+        if (!plan) throw mx::Error("mxh_new: no plan");
+        g = new Gpu(plan);
+    });
+    return reinterpret_cast<mxh_gpu *>(g);
+}
+
+void mxh_free(mxh_gpu *g) {
+    try {
+        delete G(g);
+    } catch (...) {
+    }
+}
+
+int mxh_begin(mxh_gpu *g, const mx_plan_desc *plan, const float *input, uint64_t n_in) {
+    return guard([&] {
+        G(g)->check_plan(plan);
+        const mx_bufshape &s = plan->bufs[plan->input];
+        if (n_in != (uint64_t)(s.c * s.h * s.w)) throw mx::Error("the input image and the plan's input buffer disagree");
+        if (std::getenv("MAXIM_POISON")) mxh::check(G(g)->H.hipMemsetD8Async(G(g)->arena, 0xCD, G(g)->arena_len * 4, G(g)->stream), "poison");
+        G(g)->write(plan->offs[plan->input], input, n_in);
+    });
+}
+
+int mxh_step_op(mxh_gpu *g, const mx_plan_desc *plan, uint64_t i) {
+    return guard([&] {
+        G(g)->check_plan(plan);
+        if (i >= plan->n_ops) throw mx::Error("op index out of range");
+        G(g)->run_op(i);
+        G(g)->sync();
+    });
+}
+
+int mxh_run_ops(mxh_gpu *g, const mx_plan_desc *plan, uint64_t first, uint64_t last) {
+    return guard([&] {
+        G(g)->check_plan(plan);
+        if (last > plan->n_ops || first > last) throw mx::Error("op range out of bounds");
+        for (uint64_t i = first; i < last; ++i) G(g)->run_op(i);
+    });
+}
+
+int mxh_run(mxh_gpu *g, const mx_plan_desc *plan, const float *input, uint64_t n_in, float *output, uint64_t n_out) {
+    return guard([&] {
+        Gpu &x = *G(g);
+        x.check_plan(plan);
+        const mx_bufshape &so = plan->bufs[plan->output];
+        if (n_out != (uint64_t)(so.c * so.h * so.w)) throw mx::Error("the output buffer and the plan's output disagree");
+        if (mxh_begin(g, plan, input, n_in) != 0) throw mx::Error(mx_last_error());
+        if (x.want_timeline) {
+            x.run_timed(plan->n_ops);
+        } else {
+            for (uint64_t i = 0; i < plan->n_ops; ++i) x.run_op(i);
+        }
+        x.read(plan->offs[plan->output], output, n_out);
+    });
+}
+
+int mxh_run_timed(mxh_gpu *g, const mx_plan_desc *plan) {
+    return guard([&] {
+        G(g)->check_plan(plan);
+        G(g)->run_timed(plan->n_ops);
+    });
+}
+
+int mxh_read_buf(mxh_gpu *g, const mx_plan_desc *plan, uint64_t buf, float *out, uint64_t n) {
+    return guard([&] {
+        G(g)->check_plan(plan);
+        if (buf >= plan->n_bufs) throw mx::Error("buffer index out of range");
+        const mx_bufshape &s = plan->bufs[buf];
+        if (n != (uint64_t)(s.c * s.h * s.w)) throw mx::Error("read_buf: wrong length");
+        G(g)->read(plan->offs[buf], out, n);
+    });
+}
+
+int mxh_read_into(mxh_gpu *g, uint64_t off, float *out, uint64_t n) {
+    return guard([&] { G(g)->read(off, out, n); });
+}
+
+int mxh_read_arena(mxh_gpu *g, float *out, uint64_t n) {
+    return guard([&] {
+        if (n != G(g)->arena_len) throw mx::Error("read_arena: wrong length");
+        G(g)->read(0, out, n);
+    });
+}
+
+int mxh_write_into(mxh_gpu *g, uint64_t off, const float *in, uint64_t n) {
+    return guard([&] { G(g)->write(off, in, n); });
+}
+
+int mxh_poison(mxh_gpu *g) {
+    return guard([&] {
+        mxh::check(G(g)->H.hipMemsetD8Async(G(g)->arena, 0xCD, G(g)->arena_len * 4, G(g)->stream), "poison");
+        G(g)->sync();
+    });
+}
+
+int mxh_sync(mxh_gpu *g) {
+    return guard([&] { G(g)->sync(); });
+}
+
+void mxh_set_timeline(mxh_gpu *g, int on) { G(g)->want_timeline = on != 0; }
+
+int mxh_timeline(mxh_gpu *g, float *per_op_ms, uint64_t n, float *total_ms) {
+    return guard([&] {
+        Gpu &x = *G(g);
+        if (!x.have_timeline) throw mx::Error("no timeline recorded (mxh_set_timeline, then mxh_run)");
+        if (per_op_ms) memcpy(per_op_ms, x.per_op_ms.data(), sizeof(float) * std::min<uint64_t>(n, x.per_op_ms.size()));
+        if (total_ms) *total_ms = x.total_ms;
+    });
+}
+
+int mxh_time_ops(mxh_gpu *g, const mx_plan_desc *plan, uint64_t first, uint64_t last, int iters, float *ms) {
+    return guard([&] {
+        Gpu &x = *G(g);
+        x.check_plan(plan);
+        if (last > plan->n_ops || first > last) throw mx::Error("op range out of bounds");
+        auto &H = x.H;
+        mxh::hipEvent_t a, b;
+        mxh::check(H.hipEventCreate(&a), "hipEventCreate");
+        mxh::check(H.hipEventCreate(&b), "hipEventCreate");
+        mxh::check(H.hipEventRecord(a, x.stream), "hipEventRecord");
+        for (int it = 0; it < iters; ++it)
+            for (uint64_t i = first; i < last; ++i) x.run_op(i);
+        mxh::check(H.hipEventRecord(b, x.stream), "hipEventRecord");
+        mxh::check(H.hipEventSynchronize(b), "hipEventSynchronize");
+        float t = 0.0f;
+        mxh::check(H.hipEventElapsedTime(&t, a, b), "hipEventElapsedTime");
+        H.hipEventDestroy(a);
+        H.hipEventDestroy(b);
+        if (ms) *ms = t;
+    });
+}
+
+const char *mxh_device_name(mxh_gpu *g) { return G(g)->name.c_str(); }
+uint64_t mxh_arena_bytes(mxh_gpu *g) { return G(g)->arena_len * 4; }
+uint64_t mxh_weight_bytes(mxh_gpu *g) { return G(g)->wbytes; }
+uint64_t mxh_pool_bytes(mxh_gpu *g) { return G(g)->scratch_len * 4; }
+uint64_t mxh_ops_launched(mxh_gpu *g) { return G(g)->launched; }
+uint64_t mxh_kernels_launched(mxh_gpu *g) { return G(g)->kernels; }
+
+const char *mxh_op_kernel(mxh_gpu *g, uint64_t i) {
+    Gpu &x = *G(g);
+    if (i >= x.ops.size() || x.ops[i].empty()) return "";
+    return x.ops[i][0].name;
+}
+
+int mxh_device_info(mxh_gpu *g, int *cus, int *clock_khz) {
+    if (cus) *cus = G(g)->cus;
+    if (clock_khz) *clock_khz = G(g)->clock_khz;
+    return 0;
+}
+
+}  // extern "C"

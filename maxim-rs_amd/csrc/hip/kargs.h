@@ -1,0 +1,115 @@
+// Kernel argument blocks, shared by the host executor (g++) and the gfx950
+// kernels (hipcc). Each kernel takes exactly one of these by value, so the
+// launch passes one parameter and both sides agree on the layout by
+// construction: only 8-byte fields, then 4-byte fields in pairs.
+#pragma once
+
+#include <stdint.h>
+
+#define MXK_BLOCK 256
+
+// Flat elementwise ops over n elements.
+enum { MXK_COPY = 0, MXK_ADD, MXK_MUL, MXK_GATE_APPLY, MXK_GELU, MXK_LRELU, MXK_SIGMOID };
+
+struct EwArgs {
+    const float *a;
+    const float *b;
+    float *y;
+    int64_t n;
+    int32_t op;
+    float slope;
+};
+
+// y[ch][p] = x[ch][p] * s[ch]
+struct ChanScaleArgs {
+    const float *x;
+    const float *s;
+    float *y;
+    int64_t hw;
+    int64_t c;
+};
+
+// Channel LayerNorm over [c][hw].
+struct ChanLnArgs {
+    const float *x;
+    const float *scale;
+    const float *bias;
+    float *y;
+    int64_t hw;
+    int32_t c;
+    float eps;
+};
+
+// Channel mean: partial sums per (channel, chunk) into `part`, then one
+// value per channel.
+struct ChanMeanArgs {
+    const float *x;
+    float *part;
+    float *y;
+    int64_t hw;
+    int64_t chunk;     // elements per partial
+    int32_t c;
+    int32_t nchunk;
+};
+
+// Space <-> block permutation.
+struct PermArgs {
+    const float *x;
+    float *y;
+    int64_t c;
+    int32_t h, wd, gh, gw, fh, fw, swap, forward;
+};
+
+// One axis of the jax bilinear resize. axis 2 = horizontal (rows of `n_in`
+// elements -> rows of `n_out`), axis 1 = vertical (planes of n_in rows of
+// `width` -> n_out rows).
+struct ResizeArgs {
+    const float *x;
+    float *y;
+    int64_t rows;      // horizontal: c * hin; vertical: c
+    int32_t n_in, n_out, width, axis;
+};
+
+// Nearest subsample.
+struct DownArgs {
+    const float *x;
+    float *y;
+    int64_t c;
+    int32_t h, wd, stride, off, oh, ow;
+};
+
+// C[b] = A[b] . B[b] (+ bias), A [M][K] and B [K][N] row-major, C [M][N].
+// Epilogue modes: plain (bias by row or column) or the transposed-conv scatter.
+enum { MXK_BIAS_NONE = 0, MXK_BIAS_ROW = 1, MXK_BIAS_COL = 2 };
+enum { MXK_EPI_PLAIN = 0, MXK_EPI_CONVT = 1 };
+
+struct GemmArgs {
+    const float *A;
+    const float *B;
+    const float *bias;
+    float *C;
+    int64_t sA, sB, sC;   // batch strides (elements)
+    int32_t M, N, K, batch;
+    int32_t bias_mode, epi;
+    int32_t co, wd;       // convT: output channels and input width
+};
+
+// Small GEMV for the plane-1 CALayer convs: y[o] = b[o] + sum_i w[o][i] x[i].
+struct GemvArgs {
+    const float *w;
+    const float *x;
+    const float *bias;
+    float *y;
+    int32_t ci, co;
+};
+
+// Implicit-GEMM convolution (3x3 pad 1, or 4x4 stride 2 SAME).
+// Weights are re-laid out at upload as [co][tap][ci] (K index = tap*ci + c).
+struct ConvArgs {
+    const float *x;
+    const float *w;
+    const float *bias;
+    float *y;
+    int32_t ci, co, h, wd;
+    int32_t oh, ow, pad_top, pad_left;
+};

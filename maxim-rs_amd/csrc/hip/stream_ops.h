@@ -1,0 +1,301 @@
+// Bandwidth-bound kernels: the flat elementwise family, the channel-axis ops
+// (LayerNorm, mean, scale) and the index maps (block permutation, nearest
+// subsample, bilinear resize).
+//
+// Arithmetic follows the reference's CPU arms term for term (src/exec_cpu.rs
+// 537-598, 377-434, 1075-1178) and this file is compiled without FP
+// contraction, so add / mul / gate / lrelu / chan_scale / chan_ln /
+// block_perm / down_s / resize reproduce the CPU path bit for bit; gelu and
+// sigmoid differ from it only through the device erff / expf.
+#pragma once
+
+#include "common.h"
+
+// ------------------------------------------------------------ elementwise
+
+template <int OP>
+__device__ __forceinline__ float ew1(float a, float b, float slope) {
+    if (OP == MXK_COPY) return a;
+    if (OP == MXK_ADD) return a + b;
+    if (OP == MXK_MUL) return a * b;
+    if (OP == MXK_GATE_APPLY) return a * (b + 1.0f);
+    if (OP == MXK_GELU) return 0.5f * a * (1.0f + erff(a * 0.70710678118654752440f));
+    if (OP == MXK_LRELU) return a >= 0.0f ? a : slope * a;
+    return 1.0f / (1.0f + expf(-a));  // MXK_SIGMOID
+}
+
+// Each thread moves UNROLL float4s spaced one block apart, so every load of a
+// wave is one contiguous 1 KiB run.
+template <int OP, int UNROLL>
+__device__ void ew_vec4(const EwArgs &a) {
+    const int64_t nv = a.n >> 2;
+    int64_t i = (int64_t)blockIdx.x * (MXK_BLOCK * UNROLL) + threadIdx.x;
+    float4 va[UNROLL], vb[UNROLL];
+#pragma unroll
+    for (int u = 0; u < UNROLL; ++u) {
+        int64_t j = i + u * MXK_BLOCK;
+        if (j < nv) {
+            va[u] = ld4(a.a + 4 * j);
+            if (OP == MXK_ADD || OP == MXK_MUL || OP == MXK_GATE_APPLY) vb[u] = ld4(a.b + 4 * j);
+        }
+    }
+#pragma unroll
+    for (int u = 0; u < UNROLL; ++u) {
+        int64_t j = i + u * MXK_BLOCK;
+        if (j < nv) {
+            float4 r;
+            r.x = ew1<OP>(va[u].x, vb[u].x, a.slope);
+            r.y = ew1<OP>(va[u].y, vb[u].y, a.slope);
+            r.z = ew1<OP>(va[u].z, vb[u].z, a.slope);
+            r.w = ew1<OP>(va[u].w, vb[u].w, a.slope);
+            st4(a.y + 4 * j, r);
+        }
+    }
+}
+
+template <int OP>
+__device__ void ew_scalar(const EwArgs &a) {
+    int64_t i = (int64_t)blockIdx.x * MXK_BLOCK + threadIdx.x;
+    if (i < a.n) a.y[i] = ew1<OP>(a.a[i], (OP == MXK_ADD || OP == MXK_MUL || OP == MXK_GATE_APPLY) ? a.b[i] : 0.0f, a.slope);
+}
+
+#define MXK_EW(NAME, OP)                                                                     \
+    extern "C" __global__ __launch_bounds__(MXK_BLOCK) void mx_##NAME##_v4(EwArgs a) {      \
+        ew_vec4<OP, 4>(a);                                                                   \
+    }                                                                                        \
+    extern "C" __global__ __launch_bounds__(MXK_BLOCK) void mx_##NAME##_s(EwArgs a) { ew_scalar<OP>(a); }
+
+MXK_EW(copy, MXK_COPY)
+MXK_EW(add, MXK_ADD)
+MXK_EW(mul, MXK_MUL)
+MXK_EW(gate_apply, MXK_GATE_APPLY)
+MXK_EW(gelu, MXK_GELU)
+MXK_EW(lrelu, MXK_LRELU)
+MXK_EW(sigmoid, MXK_SIGMOID)
+
+// y[ch][p] = x[ch][p] * s[ch]; grid (ceil(hw / (256 * 4 * V)), c).
+extern "C" __global__ __launch_bounds__(MXK_BLOCK) void mx_chan_scale_v4(ChanScaleArgs a) {
+    const int64_t ch = blockIdx.y;
+    const float s = a.s[ch];
+    const float *x = a.x + ch * a.hw;
+    float *y = a.y + ch * a.hw;
+    const int64_t nv = a.hw >> 2;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+        int64_t j = (int64_t)blockIdx.x * (MXK_BLOCK * 4) + u * MXK_BLOCK + threadIdx.x;
+        if (j < nv) {
+            float4 v = ld4(x + 4 * j);
+            v.x = v.x * s; v.y = v.y * s; v.z = v.z * s; v.w = v.w * s;
+            st4(y + 4 * j, v);
+        }
+    }
+}
+
+extern "C" __global__ __launch_bounds__(MXK_BLOCK) void mx_chan_scale_s(ChanScaleArgs a) {
+    const int64_t ch = blockIdx.y;
+    int64_t p = (int64_t)blockIdx.x * MXK_BLOCK + threadIdx.x;
+    if (p < a.hw) a.y[ch * a.hw + p] = a.x[ch * a.hw + p] * a.s[ch];
+}
+
+// ------------------------------------------------------------ LayerNorm
+//
+// One thread owns V adjacent pixels and holds their C channel values in
+// registers, so x is read once. Per pixel: s1, s2 in ascending channel order,
+// m = s1/c, var = s2/c - m*m, r = 1/sqrt(max(var, 0) + eps),
+// y = (x - m) * r * w + b (src/exec_cpu.rs:392-432).
+
+template <int C, int V>
+__device__ void chan_ln_body(const ChanLnArgs &a) {
+    const int64_t p0 = ((int64_t)blockIdx.x * MXK_BLOCK + threadIdx.x) * V;
+    if (p0 >= a.hw) return;
+    float v[C][V];
+    float s1[V], s2[V];
+#pragma unroll
+    for (int k = 0; k < V; ++k) { s1[k] = 0.0f; s2[k] = 0.0f; }
+#pragma unroll
+    for (int c = 0; c < C; ++c) {
+        const float *row = a.x + (int64_t)c * a.hw + p0;
+        if (V == 4) {
+            float4 q = ld4(row);
+            v[c][0] = q.x; v[c][1 % V] = q.y; v[c][2 % V] = q.z; v[c][3 % V] = q.w;
+        } else if (V == 2) {
+            float2 q = *reinterpret_cast<const float2 *>(row);
+            v[c][0] = q.x; v[c][1 % V] = q.y;
+        } else {
+            v[c][0] = row[0];
+        }
+#pragma unroll
+        for (int k = 0; k < V; ++k) {
+            s1[k] += v[c][k];
+            s2[k] += v[c][k] * v[c][k];
+        }
+    }
+    const float nf = (float)C;
+    float m[V], r[V];
+#pragma unroll
+    for (int k = 0; k < V; ++k) {
+        m[k] = s1[k] / nf;
+        float var = s2[k] / nf - m[k] * m[k];
+        r[k] = 1.0f / sqrtf(fmaxf(var, 0.0f) + a.eps);
+    }
+#pragma unroll
+    for (int c = 0; c < C; ++c) {
+        const float w = a.scale[c], b = a.bias[c];
+        float o[V];
+#pragma unroll
+        for (int k = 0; k < V; ++k) o[k] = (v[c][k] - m[k]) * r[k] * w + b;
+        float *row = a.y + (int64_t)c * a.hw + p0;
+        if (V == 4) st4(row, make_float4(o[0], o[1 % V], o[2 % V], o[3 % V]));
+        else if (V == 2) *reinterpret_cast<float2 *>(row) = make_float2(o[0], o[1 % V]);
+        else row[0] = o[0];
+    }
+}
+
+extern "C" __global__ __launch_bounds__(MXK_BLOCK) void mx_chan_ln_c32(ChanLnArgs a) { chan_ln_body<32, 4>(a); }
+extern "C" __global__ __launch_bounds__(MXK_BLOCK) void mx_chan_ln_c64(ChanLnArgs a) { chan_ln_body<64, 2>(a); }
+extern "C" __global__ __launch_bounds__(MXK_BLOCK) void mx_chan_ln_c128(ChanLnArgs a) { chan_ln_body<128, 1>(a); }
+
+// Any channel count, any alignment: reads x twice.
+extern "C" __global__ __launch_bounds__(MXK_BLOCK) void mx_chan_ln_any(ChanLnArgs a) {
+    const int64_t p = (int64_t)blockIdx.x * MXK_BLOCK + threadIdx.x;
+    if (p >= a.hw) return;
+    float s1 = 0.0f, s2 = 0.0f;
+    for (int c = 0; c < a.c; ++c) {
+        float v = a.x[(int64_t)c * a.hw + p];
+        s1 += v;
+        s2 += v * v;
+    }
+    const float nf = (float)a.c;
+    const float m = s1 / nf;
+    const float var = s2 / nf - m * m;
+    const float r = 1.0f / sqrtf(fmaxf(var, 0.0f) + a.eps);
+    for (int c = 0; c < a.c; ++c) {
+        int64_t i = (int64_t)c * a.hw + p;
+        a.y[i] = (a.x[i] - m) * r * a.scale[c] + a.bias[c];
+    }
+}
+
+// ----------------------------------------------------------- channel mean
+//
+// Two fixed-order passes: partial sums of `chunk` elements per (channel,
+// chunk), then one ordered sum of the partials per channel. Deterministic,
+// but not the CPU's serial order, so it agrees with it to rounding only.
+
+extern "C" __global__ __launch_bounds__(MXK_BLOCK) void mx_chan_mean_part(ChanMeanArgs a) {
+    __shared__ float red[MXK_BLOCK];
+    const int ch = blockIdx.y, k = blockIdx.x;
+    const float *x = a.x + (int64_t)ch * a.hw;
+    int64_t lo = (int64_t)k * a.chunk, hi = lo + a.chunk < a.hw ? lo + a.chunk : a.hw;
+    float s = 0.0f;
+    for (int64_t i = lo + threadIdx.x; i < hi; i += MXK_BLOCK) s += x[i];
+    red[threadIdx.x] = s;
+    __syncthreads();
+    for (int w = MXK_BLOCK / 2; w > 0; w >>= 1) {
+        if ((int)threadIdx.x < w) red[threadIdx.x] += red[threadIdx.x + w];
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) a.part[(int64_t)ch * a.nchunk + k] = red[0];
+}
+
+extern "C" __global__ __launch_bounds__(MXK_BLOCK) void mx_chan_mean_final(ChanMeanArgs a) {
+    const int ch = blockIdx.x * MXK_BLOCK + threadIdx.x;
+    if (ch >= a.c) return;
+    float s = 0.0f;
+    for (int k = 0; k < a.nchunk; ++k) s += a.part[(int64_t)ch * a.nchunk + k];
+    a.y[ch] = s / (float)a.hw;
+}
+
+// ------------------------------------------------------ block permutation
+//
+// Block (ch, g) moves the psz = fh * fw pixels of one cell; threads sweep p in
+// runs of V (V divides fw, so a run stays inside one pixel row). Forward
+// gathers [c][h][w] -> [c][g][p]; backward scatters it back. Pure copies.
+
+template <int V>
+__device__ void perm_body(const PermArgs &a) {
+    const int gsz = a.gh * a.gw, psz = a.fh * a.fw;
+    const int64_t e = blockIdx.x;
+    const int64_t ch = e / gsz;
+    const int g = (int)(e - ch * gsz);
+    const int gy = g / a.gw, gx = g - gy * a.gw;
+    const int64_t plane = (int64_t)a.h * a.wd;
+    const float *x = a.x + ch * plane;
+    float *y = a.y + ch * plane;
+    for (int p = threadIdx.x * V; p < psz; p += blockDim.x * V) {
+        const int fy = p / a.fw, fx = p - fy * a.fw;
+        const int64_t pix = (int64_t)(gy * a.fh + fy) * a.wd + gx * a.fw + fx;
+        const int64_t blk = a.swap ? (int64_t)p * gsz + g : (int64_t)g * psz + p;
+        if (V == 4) {
+            if (a.forward) st4(y + blk, ld4(x + pix));
+            else st4(y + pix, ld4(x + blk));
+        } else if (V == 2) {
+            if (a.forward) *reinterpret_cast<float2 *>(y + blk) = *reinterpret_cast<const float2 *>(x + pix);
+            else *reinterpret_cast<float2 *>(y + pix) = *reinterpret_cast<const float2 *>(x + blk);
+        } else {
+            if (a.forward) y[blk] = x[pix];
+            else y[pix] = x[blk];
+        }
+    }
+}
+
+extern "C" __global__ __launch_bounds__(MXK_BLOCK) void mx_block_perm_v4(PermArgs a) { perm_body<4>(a); }
+extern "C" __global__ __launch_bounds__(MXK_BLOCK) void mx_block_perm_v2(PermArgs a) { perm_body<2>(a); }
+extern "C" __global__ __launch_bounds__(MXK_BLOCK) void mx_block_perm_v1(PermArgs a) { perm_body<1>(a); }
+
+// --------------------------------------------------------- nearest subsample
+
+extern "C" __global__ __launch_bounds__(MXK_BLOCK) void mx_down_s(DownArgs a) {
+    const int64_t n = a.c * a.oh * a.ow;
+    const int64_t i = (int64_t)blockIdx.x * MXK_BLOCK + threadIdx.x;
+    if (i >= n) return;
+    const int64_t op = (int64_t)a.oh * a.ow;
+    const int64_t ch = i / op;
+    const int r = (int)(i - ch * op);
+    const int oy = r / a.ow, ox = r - oy * a.ow;
+    a.y[i] = a.x[ch * a.h * a.wd + (int64_t)(oy * a.stride + a.off) * a.wd + ox * a.stride + a.off];
+}
+
+// --------------------------------------------------------------- resize
+//
+// The tap table of each axis is built on the host by the same arithmetic as
+// the CPU's ResizeTaps (src/exec_cpu.rs:1195-1216) and handed in as
+// `x` rows of [j0, n, wsum, w0 .. w(maxt-1)] (j0 and n as floats, exact for
+// any size this engine runs). Each output is sum_k w_k * src[j0 + k] in
+// ascending k, then / wsum when wsum > 0.
+
+struct ResizeTab {
+    const float *t;
+    int32_t maxt, pad;
+};
+
+extern "C" __global__ __launch_bounds__(MXK_BLOCK) void mx_resize_h(ResizeArgs a, ResizeTab tab) {
+    const int64_t n = a.rows * a.n_out;
+    const int64_t i = (int64_t)blockIdx.x * MXK_BLOCK + threadIdx.x;
+    if (i >= n) return;
+    const int64_t r = i / a.n_out;
+    const int o = (int)(i - r * a.n_out);
+    const float *e = tab.t + (int64_t)o * (3 + tab.maxt);
+    const int j0 = (int)e[0], nt = (int)e[1];
+    const float ws = e[2];
+    const float *src = a.x + r * a.n_in + j0;
+    float acc = 0.0f;
+    for (int k = 0; k < nt; ++k) acc += e[3 + k] * src[k];
+    a.y[i] = ws > 0.0f ? acc / ws : acc;
+}
+
+extern "C" __global__ __launch_bounds__(MXK_BLOCK) void mx_resize_v(ResizeArgs a, ResizeTab tab) {
+    const int64_t n = a.rows * a.n_out * (int64_t)a.width;
+    const int64_t i = (int64_t)blockIdx.x * MXK_BLOCK + threadIdx.x;
+    if (i >= n) return;
+    const int64_t r = i / a.width;            // channel * n_out + o
+    const int x = (int)(i - r * a.width);
+    const int64_t ch = r / a.n_out;
+    const int o = (int)(r - ch * a.n_out);
+    const float *e = tab.t + (int64_t)o * (3 + tab.maxt);
+    const int j0 = (int)e[0], nt = (int)e[1];
+    const float ws = e[2];
+    const float *src = a.x + ch * a.n_in * (int64_t)a.width + (int64_t)j0 * a.width + x;
+    float acc = 0.0f;
+    for (int k = 0; k < nt; ++k) acc += e[3 + k] * src[(int64_t)k * a.width];
+    a.y[i] = ws > 0.0f ? acc / ws : acc;
+}

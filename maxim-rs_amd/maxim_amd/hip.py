@@ -1,0 +1,187 @@
+"""ctypes binding of the gfx950 executor (include/maxim_hip.h).
+
+`Gpu` mirrors the reference's `exec_gpu::Gpu` (src/exec_gpu.rs:48-357): built
+for one plan, it owns the device arena and the device weights; `run` takes an
+input image and returns the output image. There is no CPU fallback here: if
+the library or the device is missing, the call raises.
+"""
+
+import ctypes as C
+
+import numpy as np
+
+from . import plan as P
+
+_declared = False
+
+
+def _lib():
+    global _declared
+    L = P.lib()
+    if not hasattr(L, "mxh_new"):
+        raise P.MaximError("libmaxim_hip.so is not built: the HIP executor is unavailable")
+    if not _declared:
+        V, U, I = C.c_void_p, C.c_uint64, C.c_int
+        D = C.POINTER(P.PlanDesc)
+        sig = {
+            "mxh_driver_ready": (I, []),
+            "mxh_new": (V, [D]),
+            "mxh_free": (None, [V]),
+            "mxh_run": (I, [V, D, V, U, V, U]),
+            "mxh_begin": (I, [V, D, V, U]),
+            "mxh_step_op": (I, [V, D, U]),
+            "mxh_run_ops": (I, [V, D, U, U]),
+            "mxh_read_buf": (I, [V, D, U, V, U]),
+            "mxh_read_into": (I, [V, U, V, U]),
+            "mxh_read_arena": (I, [V, V, U]),
+            "mxh_write_into": (I, [V, U, V, U]),
+            "mxh_poison": (I, [V]),
+            "mxh_sync": (I, [V]),
+            "mxh_set_timeline": (None, [V, I]),
+            "mxh_timeline": (I, [V, V, U, C.POINTER(C.c_float)]),
+            "mxh_run_timed": (I, [V, D]),
+            "mxh_time_ops": (I, [V, D, U, U, I, C.POINTER(C.c_float)]),
+            "mxh_device_name": (C.c_char_p, [V]),
+            "mxh_arena_bytes": (U, [V]),
+            "mxh_weight_bytes": (U, [V]),
+            "mxh_pool_bytes": (U, [V]),
+            "mxh_ops_launched": (U, [V]),
+            "mxh_kernels_launched": (U, [V]),
+            "mxh_op_kernel": (C.c_char_p, [V, U]),
+            "mxh_device_info": (I, [V, C.POINTER(C.c_int), C.POINTER(C.c_int)]),
+        }
+        for name, (res, args) in sig.items():
+            f = getattr(L, name)
+            f.restype = res
+            f.argtypes = args
+        _declared = True
+    return L
+
+
+def _check(rc):
+    if rc != 0:
+        raise P.MaximError(P.last_error())
+
+
+def driver_ready():
+    """exec_gpu::driver_ready: True when the HIP runtime and a device come up."""
+    return _lib().mxh_driver_ready() == 0
+
+
+class Gpu:
+    def __init__(self, plan):
+        L = _lib()
+        self.plan = plan
+        self._d = C.byref(plan.desc)
+        self._h = L.mxh_new(self._d)
+        if not self._h:
+            raise P.MaximError(P.last_error())
+
+    def close(self):
+        if getattr(self, "_h", None):
+            _lib().mxh_free(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def run(self, image):
+        img = np.ascontiguousarray(image, dtype=np.float32)
+        c, h, w = self.plan.bufs[self.plan.output]
+        out = np.empty((c, h, w), np.float32)
+        _check(_lib().mxh_run(self._h, self._d, img.ctypes.data, img.size, out.ctypes.data, out.size))
+        return out
+
+    def begin(self, image):
+        img = np.ascontiguousarray(image, dtype=np.float32)
+        _check(_lib().mxh_begin(self._h, self._d, img.ctypes.data, img.size))
+
+    def step_op(self, i):
+        _check(_lib().mxh_step_op(self._h, self._d, i))
+
+    def run_ops(self, first, last):
+        _check(_lib().mxh_run_ops(self._h, self._d, first, last))
+
+    def read_buf(self, buf):
+        n = self.plan.buf_len(buf)
+        out = np.empty(n, np.float32)
+        _check(_lib().mxh_read_buf(self._h, self._d, buf, out.ctypes.data, n))
+        return out
+
+    def read_into(self, off, n):
+        out = np.empty(n, np.float32)
+        _check(_lib().mxh_read_into(self._h, off, out.ctypes.data, n))
+        return out
+
+    def write_into(self, off, data):
+        d = np.ascontiguousarray(data, dtype=np.float32)
+        _check(_lib().mxh_write_into(self._h, off, d.ctypes.data, d.size))
+
+    def write_buf(self, buf, data):
+        self.write_into(int(self.plan.offs[buf]), data)
+
+    def read_arena(self):
+        out = np.empty(self.plan.arena_len, np.float32)
+        _check(_lib().mxh_read_arena(self._h, out.ctypes.data, out.size))
+        return out
+
+    def poison(self):
+        _check(_lib().mxh_poison(self._h))
+
+    def sync(self):
+        _check(_lib().mxh_sync(self._h))
+
+    def set_timeline(self, on=True):
+        _lib().mxh_set_timeline(self._h, int(on))
+
+    def timeline(self):
+        n = len(self.plan.ops)
+        per = np.empty(n, np.float32)
+        tot = C.c_float()
+        _check(_lib().mxh_timeline(self._h, per.ctypes.data, n, C.byref(tot)))
+        return per, tot.value
+
+    def run_timed(self):
+        """Every op over the resident input, one event per op: (per-op ms, total ms)."""
+        _check(_lib().mxh_run_timed(self._h, self._d))
+        return self.timeline()
+
+    def time_ops(self, first, last, iters=1):
+        ms = C.c_float()
+        _check(_lib().mxh_time_ops(self._h, self._d, first, last, iters, C.byref(ms)))
+        return ms.value
+
+    def op_kernel(self, i):
+        return _lib().mxh_op_kernel(self._h, i).decode()
+
+    @property
+    def device_name(self):
+        return _lib().mxh_device_name(self._h).decode()
+
+    @property
+    def arena_bytes(self):
+        return _lib().mxh_arena_bytes(self._h)
+
+    @property
+    def weight_bytes(self):
+        return _lib().mxh_weight_bytes(self._h)
+
+    @property
+    def pool_bytes(self):
+        return _lib().mxh_pool_bytes(self._h)
+
+    @property
+    def ops_launched(self):
+        return _lib().mxh_ops_launched(self._h)
+
+    @property
+    def kernels_launched(self):
+        return _lib().mxh_kernels_launched(self._h)
+
+    def device_info(self):
+        cu, clk = C.c_int(), C.c_int()
+        _lib().mxh_device_info(self._h, C.byref(cu), C.byref(clk))
+        return cu.value, clk.value

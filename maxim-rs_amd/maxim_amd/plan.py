@@ -296,3 +296,60 @@ def crop_out(img, p):
     _check(lib().mx_crop_out(img.ctypes.data, c, ph, pw, p.even_h, p.even_w, p.orig_h, p.orig_w,
                              out.ctypes.data))
     return out
+
+
+def make_op(kind, **kw):
+    """An Op with every index field at -1 unless given."""
+    o = Op()
+    o.kind = kind
+    for f in ("dst", "src", "src2", "w", "wt", "bias", "scale"):
+        setattr(o, f, -1)
+    for k, v in kw.items():
+        if k == "p":
+            for i, x in enumerate(v):
+                o.p[i] = x
+        else:
+            setattr(o, k, v)
+    return o
+
+
+class CustomPlan:
+    """A plan assembled by hand: buffers packed back to back, one op list.
+
+    This is what any host that owns its own plan does at the boundary: fill an
+    mx_plan_desc from its own arrays. Used for the isolated-op configurations.
+    """
+
+    def __init__(self, bufs, ops, weights, input=0, output=None, align=64):
+        self.bufs = [tuple(int(v) for v in b) for b in bufs]
+        offs, off = [], 0
+        for c, h, w in self.bufs:
+            offs.append(off)
+            off += c * h * w
+            off = (off + align - 1) // align * align
+        self.offs = np.array(offs, np.uint64)
+        self.arena_len = max(off, 1)
+        self.ops = list(ops)
+        self.input = input
+        self.output = output if output is not None else ops[-1].dst
+        self._weights = [np.ascontiguousarray(w, dtype=np.float32).ravel() for w in weights]
+        self._ops = (Op * max(len(ops), 1))(*ops)
+        self._bufs = (BufShape * len(bufs))(*[BufShape(*b) for b in self.bufs])
+        self._offs = (C.c_uint64 * len(offs))(*[int(x) for x in offs])
+        nw = max(len(self._weights), 1)
+        self._wptr = (C.POINTER(C.c_float) * nw)(*[w.ctypes.data_as(C.POINTER(C.c_float)) for w in self._weights])
+        self._wlen = (C.c_uint64 * nw)(*[w.size for w in self._weights])
+        d = PlanDesc()
+        d.n_ops, d.ops = len(ops), self._ops
+        d.n_bufs, d.bufs, d.offs = len(bufs), self._bufs, self._offs
+        d.n_weights, d.weights, d.weight_lens = len(self._weights), self._wptr, self._wlen
+        d.arena_len, d.input, d.output = self.arena_len, self.input, self.output
+        self.desc = d
+        self.shape = self.bufs[self.input]
+
+    def buf_len(self, i):
+        c, h, w = self.bufs[i]
+        return c * h * w
+
+    def weight(self, i):
+        return self._weights[i]
