@@ -149,6 +149,8 @@ int mx_weights_save(const mx_weights *w, const char *path, const char *task);
 int mx_weights_config(const mx_weights *w, mx_config *out);
 uint64_t mx_weights_count(const mx_weights *w);
 uint64_t mx_weights_params(const mx_weights *w);
+/* The i-th tensor name in sorted order (the file's order), NULL past the end. */
+const char *mx_weights_name(const mx_weights *w, uint64_t i);
 /* One tensor by name: returns its element count (0 if absent); `shape` gets up to 4 dims. */
 uint64_t mx_weights_tensor(const mx_weights *w, const char *name, const float **data,
                            int64_t shape[4], int32_t *ndim);

@@ -1,6 +1,7 @@
 // The C ABI over the plan contract (include/maxim_plan.h).
 
 #include <cstring>
+#include <iterator>
 #include <string>
 
 #include "host.hpp"
@@ -72,6 +73,14 @@ uint64_t mx_weights_count(const mx_weights *w) {
 
 uint64_t mx_weights_params(const mx_weights *w) {
     return reinterpret_cast<const Weights *>(w)->params();
+}
+
+const char *mx_weights_name(const mx_weights *w, uint64_t i) {
+    auto &t = reinterpret_cast<const Weights *>(w)->tensors;
+    if (i >= t.size()) return nullptr;
+    auto it = t.begin();
+    std::advance(it, (long)i);
+    return it->first.c_str();
 }
 
 uint64_t mx_weights_tensor(const mx_weights *w, const char *name, const float **data,

@@ -91,6 +91,7 @@ def _declare(lib):
         "mx_weights_config": (C.c_int, [P, C.POINTER(Config)]),
         "mx_weights_count": (C.c_uint64, [P]),
         "mx_weights_params": (C.c_uint64, [P]),
+        "mx_weights_name": (C.c_char_p, [P, C.c_uint64]),
         "mx_weights_tensor": (C.c_uint64, [P, C.c_char_p, C.POINTER(C.POINTER(C.c_float)),
                                            C.POINTER(C.c_int64), C.POINTER(C.c_int32)]),
         "mx_weights_free": (V, [P]),
@@ -180,6 +181,14 @@ class Weights:
     @property
     def params(self):
         return lib().mx_weights_params(self._h)
+
+    def names(self):
+        L = lib()
+        return [L.mx_weights_name(self._h, i).decode() for i in range(self.count)]
+
+    def flat(self):
+        """Every tensor, Flax layout, as a name -> ndarray dict."""
+        return {n: self.tensor(n) for n in self.names()}
 
     def tensor(self, name):
         data = C.POINTER(C.c_float)()
