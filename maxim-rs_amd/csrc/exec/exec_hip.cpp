@@ -122,6 +122,73 @@ struct ResizeTab {
     int32_t maxt, pad;
 };
 
+// The GEMM tile for an M x N problem (times `batch`): estimated time is the
+// number of rounds of resident blocks (two per CU) times the tile's cost,
+// where bigger tiles do more work per byte staged. Every tile reduces K in the
+// same order, so the choice never changes a bit of the result.
+struct Tile {
+    int bm, bn;
+};
+
+Tile pick_tile(int64_t M, int64_t N, int64_t batch, int cus) {
+    static const struct {
+        int bm, bn;
+        double eff;
+    } cand[] = {{128, 128, 1.00}, {64, 128, 0.85}, {128, 64, 0.85},
+                {64, 64, 0.70},   {32, 128, 0.70}, {32, 64, 0.55}};
+    const int64_t slots = 2LL * (cus > 0 ? cus : 256);
+    double best = 1e300;
+    Tile t{128, 128};
+    for (auto &c : cand) {
+        int64_t blocks = ((M + c.bm - 1) / c.bm) * ((N + c.bn - 1) / c.bn) * batch;
+        double rounds = (double)((blocks + slots - 1) / slots);
+        double cost = rounds * c.bm * c.bn / c.eff;
+        if (cost < best * 0.999) {
+            best = cost;
+            t = Tile{c.bm, c.bn};
+        }
+    }
+    return t;
+}
+
+std::string gemm_name(Tile t, bool vec) {
+    return "mx_gemm_" + std::to_string(t.bm) + "x" + std::to_string(t.bn) + (vec ? "_v4" : "");
+}
+
+// The implicit-GEMM conv tile: BM output channels x TH x 16 outputs, CK input
+// channels per LDS chunk (4 for the few-channel RGB convs and every 4x4).
+// Same cost model as the GEMM tile.
+struct ConvCfg {
+    int bm = 0, th = 0, ck = 0;
+};
+
+ConvCfg pick_conv(int64_t co, int64_t ci, int64_t oh, int64_t ow, bool k3, int cus) {
+    static const struct {
+        int bm, th;
+        double eff;
+    } cand[] = {{128, 8, 1.00}, {64, 8, 0.85}, {128, 4, 0.85}, {64, 4, 0.70}, {32, 8, 0.70}, {32, 4, 0.55}};
+    const int64_t slots = 2LL * (cus > 0 ? cus : 256);
+    double best = 1e300;
+    ConvCfg r;
+    for (auto &c : cand) {
+        int64_t blocks = ((co + c.bm - 1) / c.bm) * ((oh + c.th - 1) / c.th) * ((ow + 15) / 16);
+        double rounds = (double)((blocks + slots - 1) / slots);
+        double cost = rounds * c.bm * c.th * 16 / c.eff;
+        if (cost < best * 0.999) {
+            best = cost;
+            r.bm = c.bm;
+            r.th = c.th;
+        }
+    }
+    r.ck = (k3 && ci > 4) ? 8 : 4;
+    return r;
+}
+
+std::string conv_name(ConvCfg c, bool k3) {
+    return std::string(k3 ? "mx_conv3x3_m" : "mx_conv4x4_m") + std::to_string(c.bm) + "_t" + std::to_string(c.th) +
+           (k3 && c.ck == 4 ? "_c4" : "");
+}
+
 }  // namespace
 
 class Gpu {
@@ -197,6 +264,7 @@ public:
     }
 
 private:
+    std::vector<ConvCfg> ccfg;
     std::map<std::string, hipFunction_t> fns_;
     std::set<std::string> names_;
     const char *intern(const std::string &s) { return names_.insert(s).first->c_str(); }
@@ -359,6 +427,7 @@ Gpu::Gpu(const mx_plan_desc *p) : H(hip()) {
     };
     std::vector<std::array<int64_t, 4>> extra(p->n_ops, {-1, -1, -1, -1});  // per-op derived blobs
     std::vector<std::array<int, 2>> maxt(p->n_ops, {0, 0});
+    ccfg.assign(p->n_ops, ConvCfg{});
     uint64_t mean_scratch = 0;
     for (uint64_t i = 0; i < p->n_ops; ++i) {
         const mx_op &o = p->ops[i];
@@ -379,14 +448,23 @@ Gpu::Gpu(const mx_plan_desc *p) : H(hip()) {
                 break;
             case MX_OP_CONV3X3:
             case MX_OP_CONV4X4S2: {
-                // [co][ci][k][k] -> [co][tap][ci]
-                const int taps = o.kind == MX_OP_CONV3X3 ? 9 : 16;
+                // [co][ci][k][k] -> the kernel's LDS tiles, [m-block][chunk][tap*CK + c][BM]
+                const bool k3 = o.kind == MX_OP_CONV3X3;
+                const int taps = k3 ? 9 : 16;
+                const ConvCfg cc = pick_conv(o.c_out, o.c_in, k3 ? o.h : o.oh, k3 ? o.wd : o.ow, k3, cus);
+                ccfg[i] = cc;
                 const float *w = p->weights[o.w];
-                std::vector<float> t((size_t)(o.c_out * o.c_in * taps));
-                for (int64_t m = 0; m < o.c_out; ++m)
-                    for (int64_t c = 0; c < o.c_in; ++c)
-                        for (int tp = 0; tp < taps; ++tp)
-                            t[(m * taps + tp) * o.c_in + c] = w[(m * o.c_in + c) * taps + tp];
+                const int64_t nmb = (o.c_out + cc.bm - 1) / cc.bm, nch = (o.c_in + cc.ck - 1) / cc.ck;
+                const int64_t kc = (int64_t)taps * cc.ck;
+                std::vector<float> t((size_t)(nmb * nch * kc * cc.bm), 0.0f);
+                for (int64_t mb = 0; mb < nmb; ++mb)
+                    for (int64_t ch = 0; ch < nch; ++ch)
+                        for (int64_t k = 0; k < kc; ++k)
+                            for (int64_t m = 0; m < cc.bm; ++m) {
+                                const int64_t gm = mb * cc.bm + m, gc = ch * cc.ck + k % cc.ck, tp = k / cc.ck;
+                                if (gm < o.c_out && gc < o.c_in)
+                                    t[((mb * nch + ch) * kc + k) * cc.bm + m] = w[(gm * o.c_in + gc) * taps + tp];
+                            }
                 extra[i][0] = placev(t);
                 as_is(o.bias);
                 break;
@@ -520,12 +598,13 @@ void Gpu::build_launches(const mx_plan_desc *p, const std::vector<int64_t> &woff
             case MX_OP_CHAN_LN: {
                 ChanLnArgs a{B(o.src), W(o.scale), W(o.bias), B(o.dst), o.hw, (int32_t)o.c, mx::kEps};
                 const char *k = "mx_chan_ln_any";
-                int v = 1;
-                if (o.c == 32 && o.hw % 4 == 0 && aligned(a.x, 16) && aligned(a.y, 16)) { k = "mx_chan_ln_c32"; v = 4; }
-                else if (o.c == 64 && o.hw % 2 == 0 && aligned(a.x, 8) && aligned(a.y, 8)) { k = "mx_chan_ln_c64"; v = 2; }
-                else if (o.c == 128) { k = "mx_chan_ln_c128"; v = 1; }
+                int64_t per = MXK_BLOCK;  // pixels per block
+                const bool vec = o.hw % 4 == 0 && aligned(a.x, 16) && aligned(a.y, 16);
+                if (vec && o.c == 32) { k = "mx_chan_ln_c32"; per = 256; }
+                else if (vec && o.c == 64) { k = "mx_chan_ln_c64"; per = 128; }
+                else if (vec && o.c == 128) { k = "mx_chan_ln_c128"; per = 64; }
                 Launch l = mk(k);
-                l.g[0] = cdiv(o.hw / v, MXK_BLOCK);
+                l.g[0] = cdiv(o.hw, per);
                 set_args(l, a);
                 L.push_back(l);
                 break;
@@ -567,14 +646,10 @@ void Gpu::build_launches(const mx_plan_desc *p, const std::vector<int64_t> &woff
                 a.bias_mode = o.bias >= 0 ? MXK_BIAS_ROW : MXK_BIAS_NONE;
                 a.epi = MXK_EPI_PLAIN;
                 if (plane > 0x7fffffff) throw Error("conv1x1 plane too large");
-                bool vec = plane % 4 == 0 && aligned(a.B, 16);
-                int bm = o.c_out <= 32 ? 32 : o.c_out <= 64 ? 64 : 128;
-                const char *k = bm == 32 ? (vec ? "mx_gemm_32x128_v4" : "mx_gemm_32x128")
-                                : bm == 64 ? (vec ? "mx_gemm_64x128_v4" : "mx_gemm_64x128")
-                                           : (vec ? "mx_gemm_128x128_v4" : "mx_gemm_128x128");
-                Launch l = mk(k);
-                l.g[0] = cdiv(plane, 128);
-                l.g[1] = grid_yz((o.c_out + bm - 1) / bm);
+                Tile t = pick_tile(o.c_out, plane, 1, cus);
+                Launch l = mk(gemm_name(t, o.c_in % 4 == 0 && aligned(a.A, 16)));
+                l.g[0] = cdiv(plane, t.bn);
+                l.g[1] = grid_yz((o.c_out + t.bm - 1) / t.bm);
                 set_args(l, a);
                 L.push_back(l);
                 break;
@@ -595,13 +670,11 @@ void Gpu::build_launches(const mx_plan_desc *p, const std::vector<int64_t> &woff
                 a.ow = (int32_t)(k3 ? o.wd : o.ow);
                 a.pad_top = (int32_t)(k3 ? 1 : o.p[0]);
                 a.pad_left = (int32_t)(k3 ? 1 : o.p[1]);
-                int bm = o.c_out <= 32 ? 32 : o.c_out <= 64 ? 64 : 128;
-                std::string k = std::string(k3 ? "mx_conv3x3_m" : "mx_conv4x4_m") + std::to_string(bm);
-                if (k3 && o.c_in <= 4) k += "_c4";
-                Launch l = mk(k);
-                const int64_t tiles = (int64_t)((a.oh + 7) / 8) * ((a.ow + 15) / 16);
+                const ConvCfg &cc = ccfg[i];
+                Launch l = mk(conv_name(cc, k3));
+                const int64_t tiles = (int64_t)((a.oh + cc.th - 1) / cc.th) * ((a.ow + 15) / 16);
                 l.g[0] = cdiv(tiles, 1);
-                l.g[1] = grid_yz((o.c_out + bm - 1) / bm);
+                l.g[1] = grid_yz((o.c_out + cc.bm - 1) / cc.bm);
                 set_args(l, a);
                 L.push_back(l);
                 break;
@@ -621,10 +694,10 @@ void Gpu::build_launches(const mx_plan_desc *p, const std::vector<int64_t> &woff
                 a.epi = MXK_EPI_CONVT;
                 a.co = (int32_t)o.c_out;
                 a.wd = (int32_t)o.wd;
-                bool vec = plane % 4 == 0 && aligned(a.B, 16);
-                Launch l = mk(vec ? "mx_gemm_128x128_v4" : "mx_gemm_128x128");
-                l.g[0] = cdiv(plane, 128);
-                l.g[1] = grid_yz((a.M + 127) / 128);
+                Tile t = pick_tile(a.M, plane, 1, cus);
+                Launch l = mk(gemm_name(t, o.c_in % 4 == 0 && aligned(a.A, 16)));
+                l.g[0] = cdiv(plane, t.bn);
+                l.g[1] = grid_yz((a.M + t.bm - 1) / t.bm);
                 set_args(l, a);
                 L.push_back(l);
                 break;
@@ -646,13 +719,10 @@ void Gpu::build_launches(const mx_plan_desc *p, const std::vector<int64_t> &woff
                     a.N = (int32_t)inner;
                     a.batch = (int32_t)o.c;
                     a.bias_mode = o.bias >= 0 ? MXK_BIAS_ROW : MXK_BIAS_NONE;
-                    bool vec = inner % 4 == 0 && aligned(a.B, 16);
-                    int bm = outer <= 64 ? 64 : 128;
-                    const char *k = bm == 64 ? (vec ? "mx_gemm_64x128_v4" : "mx_gemm_64x128")
-                                             : (vec ? "mx_gemm_128x128_v4" : "mx_gemm_128x128");
-                    Launch l = mk(k);
-                    l.g[0] = cdiv(inner, 128);
-                    l.g[1] = grid_yz((outer + bm - 1) / bm);
+                    Tile t = pick_tile(outer, inner, o.c, cus);
+                    Launch l = mk(gemm_name(t, outer % 4 == 0 && aligned(a.A, 16)));
+                    l.g[0] = cdiv(inner, t.bn);
+                    l.g[1] = grid_yz((outer + t.bm - 1) / t.bm);
                     l.g[2] = grid_yz(o.c);
                     set_args(l, a);
                     L.push_back(l);
@@ -666,12 +736,10 @@ void Gpu::build_launches(const mx_plan_desc *p, const std::vector<int64_t> &woff
                     a.batch = 1;
                     a.bias_mode = o.bias >= 0 ? MXK_BIAS_COL : MXK_BIAS_NONE;
                     if (o.c * outer > 0x7fffffff) throw Error("gate_mm rows too many");
-                    bool wide = inner > 64;
-                    const char *k = wide ? "mx_gemm_128x128_v4" : "mx_gemm_128x64_v4";
-                    if (inner % 4 != 0) k = wide ? "mx_gemm_128x128" : "mx_gemm_128x64";
-                    Launch l = mk(k);
-                    l.g[0] = cdiv(inner, wide ? 128 : 64);
-                    l.g[1] = grid_yz((a.M + 127) / 128);
+                    Tile t = pick_tile(a.M, inner, 1, cus);
+                    Launch l = mk(gemm_name(t, inner % 4 == 0 && aligned(a.A, 16)));
+                    l.g[0] = cdiv(inner, t.bn);
+                    l.g[1] = grid_yz((a.M + t.bm - 1) / t.bm);
                     set_args(l, a);
                     L.push_back(l);
                 }

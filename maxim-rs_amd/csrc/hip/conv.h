@@ -1,47 +1,81 @@
 // Implicit-GEMM convolutions on the fp32 matrix cores: 3x3 pad 1 and 4x4
 // stride 2 (flax SAME). out[m][p] = b[m] + sum_{tap, c} W[m][tap][c] * x[c][p + tap]
-// with zero padding. Weights arrive re-laid out as [co][tap][ci].
+// with zero padding.
 //
-// A block owns BM output channels x a TH x TW output tile. Per chunk of CK
-// input channels it stages the weight slice (k-major) and the input halo of
-// the tile (planar [c][rows][cols], zero outside the image) in LDS; the B
-// operand of every MFMA is read straight from the halo, so each input
-// element is fetched from memory once per (tile, m-block) instead of
-// once per tap.
+// A block owns BM output channels x a TH x TW output tile, and walks the
+// input channels in chunks of CK. Per chunk it stages in LDS
+//   - the weight slice, which the host has already laid out as the exact
+//     [KC][BM] tile (KC = taps * CK, k = tap * CK + c) of each (m-block,
+//     chunk), so the fill is a straight 128-bit copy;
+//   - the input halo of the tile, planar [c][rows][cols], zero outside the
+//     image;
+// and the B operand of every MFMA is read straight from the halo, so an input
+// element is fetched from memory once per (tile, m-block), not once per tap.
+// The next chunk is fetched into registers while the current one is multiplied.
 #pragma once
 
 #include "common.h"
 
+namespace conv {
+
 template <int BM, int TH, int TW, int CK, int KS, int STRIDE, int WAVES_M, int WAVES_N>
-__device__ void conv_body(const ConvArgs &a) {
+__device__ void body(const ConvArgs &a) {
     constexpr int TAPS = KS * KS;
     constexpr int KC = TAPS * CK;
     constexpr int BN = TH * TW;
     constexpr int HH = (TH - 1) * STRIDE + KS, HW = (TW - 1) * STRIDE + KS;
+    constexpr int HALO = CK * HH * HW;
     constexpr int WTM = BM / WAVES_M, WTN = BN / WAVES_N;
     constexpr int TM = WTM / 16, TN = WTN / 16;
-    static_assert(KC % 4 == 0, "K chunk must be a multiple of the MFMA K");
-    static_assert(WAVES_M * WAVES_N == 4, "4 waves");
-    __shared__ float Ws[KC][BM + 4];
-    __shared__ float Hs[CK][HH][HW];
+    constexpr int LDM = BM + 4;
+    constexpr int NW4 = KC * BM / 4;                // float4s in the weight tile
+    constexpr int NW = (NW4 + 255) / 256;           // ... per thread
+    constexpr int NH = (HALO + 255) / 256;          // halo elements per thread
+    static_assert(KC % 4 == 0 && BM % 16 == 0, "weight tile");
+    static_assert(WAVES_M * WAVES_N == 4 && TM >= 1 && TN >= 1, "wave grid");
+    __shared__ float Ws[KC][LDM];
+    __shared__ float Hs[HALO];
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wm = wave / WAVES_N, wn = wave % WAVES_N;
     const int lr = lane & 15, lk = lane >> 4;
     const int tiles_x = (a.ow + TW - 1) / TW;
     const int ty0 = (blockIdx.x / tiles_x) * TH, tx0 = (blockIdx.x % tiles_x) * TW;
-    const int m0 = blockIdx.y * BM;
+    const int mb = blockIdx.y, m0 = mb * BM;
     const int iy0 = ty0 * STRIDE - a.pad_top, ix0 = tx0 * STRIDE - a.pad_left;
     const int64_t plane = (int64_t)a.h * a.wd;
+    const int nchunk = (a.ci + CK - 1) / CK;
+    const float *wblk = a.w + (int64_t)mb * nchunk * (KC * BM);
 
     // The halo offset of each B column this lane reads, fixed for the block.
     int nofs[TN];
 #pragma unroll
     for (int j = 0; j < TN; ++j) {
         const int n = wn * WTN + j * 16 + lr;
-        const int ty = n / TW, tx = n % TW;
-        nofs[j] = ty * STRIDE * HW + tx * STRIDE;
+        nofs[j] = (n / TW) * STRIDE * HW + (n % TW) * STRIDE;
     }
+
+    float4 wr[NW];
+    float hr[NH];
+    auto fetch = [&](int chunk) {
+        const float4 *src = reinterpret_cast<const float4 *>(wblk + (int64_t)chunk * (KC * BM));
+#pragma unroll
+        for (int i = 0; i < NW; ++i)
+            if (tid + i * 256 < NW4) wr[i] = src[tid + i * 256];
+        const int c0 = chunk * CK;
+#pragma unroll
+        for (int i = 0; i < NH; ++i) {
+            const int e = tid + i * 256;
+            float v = 0.0f;
+            if (e < HALO) {
+                const int c = e / (HH * HW), r = e % (HH * HW);
+                const int iy = iy0 + r / HW, ix = ix0 + r % HW;
+                if (c0 + c < a.ci && iy >= 0 && iy < a.h && ix >= 0 && ix < a.wd)
+                    v = a.x[(c0 + c) * plane + (int64_t)iy * a.wd + ix];
+            }
+            hr[i] = v;
+        }
+    };
 
     f32x4 acc[TM][TN];
 #pragma unroll
@@ -49,28 +83,26 @@ __device__ void conv_body(const ConvArgs &a) {
 #pragma unroll
         for (int j = 0; j < TN; ++j) acc[i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 
-    for (int c0 = 0; c0 < a.ci; c0 += CK) {
-        for (int i = tid; i < KC * BM; i += 256) {
-            const int m = i / KC, k = i % KC;
-            const int tap = k / CK, c = k % CK;
-            const int gm = m0 + m, gc = c0 + c;
-            Ws[k][m] = (gm < a.co && gc < a.ci) ? a.w[((int64_t)gm * TAPS + tap) * a.ci + gc] : 0.0f;
+    fetch(0);
+    for (int chunk = 0; chunk < nchunk; ++chunk) {
+        __syncthreads();
+#pragma unroll
+        for (int i = 0; i < NW; ++i) {
+            const int e = (tid + i * 256) * 4;
+            if (e < KC * BM) st4(&Ws[e / BM][e % BM], wr[i]);
         }
-        for (int i = tid; i < CK * HH * HW; i += 256) {
-            const int c = i / (HH * HW), r = i % (HH * HW);
-            const int hy = r / HW, hx = r % HW;
-            const int gc = c0 + c, iy = iy0 + hy, ix = ix0 + hx;
-            float v = 0.0f;
-            if (gc < a.ci && iy >= 0 && iy < a.h && ix >= 0 && ix < a.wd) v = a.x[gc * plane + (int64_t)iy * a.wd + ix];
-            Hs[c][hy][hx] = v;
+#pragma unroll
+        for (int i = 0; i < NH; ++i) {
+            const int e = tid + i * 256;
+            if (e < HALO) Hs[e] = hr[i];
         }
         __syncthreads();
-#pragma unroll 4
+        if (chunk + 1 < nchunk) fetch(chunk + 1);
+#pragma unroll 2
         for (int kk = 0; kk < KC; kk += 4) {
             const int k = kk + lk;
             const int tap = k / CK, c = k % CK;
-            const int ky = tap / KS, kx = tap % KS;
-            const float *hb = &Hs[c][ky][kx];
+            const float *hb = &Hs[c * (HH * HW) + (tap / KS) * HW + (tap % KS)];
             float af[TM], bf[TN];
 #pragma unroll
             for (int i = 0; i < TM; ++i) af[i] = Ws[k][wm * WTM + i * 16 + lr];
@@ -81,7 +113,6 @@ __device__ void conv_body(const ConvArgs &a) {
 #pragma unroll
                 for (int j = 0; j < TN; ++j) acc[i][j] = mfma16(af[i], bf[j], acc[i][j]);
         }
-        __syncthreads();
     }
 
     const int64_t oplane = (int64_t)a.oh * a.ow;
@@ -104,34 +135,36 @@ __device__ void conv_body(const ConvArgs &a) {
     }
 }
 
-// 3x3 pad 1: tile 8 x 16 outputs.
-extern "C" __global__ __launch_bounds__(256) void mx_conv3x3_m32(ConvArgs a) {
-    conv_body<32, 8, 16, 8, 3, 1, 1, 4>(a);
-}
-extern "C" __global__ __launch_bounds__(256) void mx_conv3x3_m64(ConvArgs a) {
-    conv_body<64, 8, 16, 8, 3, 1, 2, 2>(a);
-}
-extern "C" __global__ __launch_bounds__(256) void mx_conv3x3_m128(ConvArgs a) {
-    conv_body<128, 8, 16, 8, 3, 1, 2, 2>(a);
-}
-// Few input channels (the RGB input convs): CK = 4.
-extern "C" __global__ __launch_bounds__(256) void mx_conv3x3_m32_c4(ConvArgs a) {
-    conv_body<32, 8, 16, 4, 3, 1, 1, 4>(a);
-}
-extern "C" __global__ __launch_bounds__(256) void mx_conv3x3_m64_c4(ConvArgs a) {
-    conv_body<64, 8, 16, 4, 3, 1, 2, 2>(a);
-}
-extern "C" __global__ __launch_bounds__(256) void mx_conv3x3_m128_c4(ConvArgs a) {
-    conv_body<128, 8, 16, 4, 3, 1, 2, 2>(a);
-}
+}  // namespace conv
 
-// 4x4 stride 2 SAME: tile 8 x 16 outputs over an 18 x 34 input halo.
-extern "C" __global__ __launch_bounds__(256) void mx_conv4x4_m32(ConvArgs a) {
-    conv_body<32, 8, 16, 4, 4, 2, 1, 4>(a);
-}
-extern "C" __global__ __launch_bounds__(256) void mx_conv4x4_m64(ConvArgs a) {
-    conv_body<64, 8, 16, 4, 4, 2, 2, 2>(a);
-}
-extern "C" __global__ __launch_bounds__(256) void mx_conv4x4_m128(ConvArgs a) {
-    conv_body<128, 8, 16, 4, 4, 2, 2, 2>(a);
-}
+// mx_conv3x3_m<BM>_t<TH>[_c4]: BM output channels x a TH x 16 output tile,
+// CK = 8 input channels per chunk (4 for the _c4 RGB-input forms).
+#define MXK_CONV3(BM, TH, CK, WM, WN, SUF)                                                      \
+    extern "C" __global__ __launch_bounds__(256) void mx_conv3x3_m##BM##_t##TH##SUF(ConvArgs a) { \
+        conv::body<BM, TH, 16, CK, 3, 1, WM, WN>(a);                                            \
+    }
+MXK_CONV3(32, 8, 8, 1, 4, )
+MXK_CONV3(64, 8, 8, 2, 2, )
+MXK_CONV3(128, 8, 8, 2, 2, )
+MXK_CONV3(32, 4, 8, 2, 2, )
+MXK_CONV3(64, 4, 8, 2, 2, )
+MXK_CONV3(128, 4, 8, 4, 1, )
+MXK_CONV3(32, 8, 4, 1, 4, _c4)
+MXK_CONV3(64, 8, 4, 2, 2, _c4)
+MXK_CONV3(128, 8, 4, 2, 2, _c4)
+MXK_CONV3(32, 4, 4, 2, 2, _c4)
+MXK_CONV3(64, 4, 4, 2, 2, _c4)
+MXK_CONV3(128, 4, 4, 4, 1, _c4)
+
+// mx_conv4x4_m<BM>_t<TH>: 4x4 stride 2 SAME, CK = 4, TH x 16 outputs over a
+// (2 TH + 2) x 34 input halo.
+#define MXK_CONV4(BM, TH, WM, WN)                                                               \
+    extern "C" __global__ __launch_bounds__(256) void mx_conv4x4_m##BM##_t##TH(ConvArgs a) {    \
+        conv::body<BM, TH, 16, 4, 4, 2, WM, WN>(a);                                             \
+    }
+MXK_CONV4(32, 8, 1, 4)
+MXK_CONV4(64, 8, 2, 2)
+MXK_CONV4(128, 8, 2, 2)
+MXK_CONV4(32, 4, 2, 2)
+MXK_CONV4(64, 4, 2, 2)
+MXK_CONV4(128, 4, 4, 1)

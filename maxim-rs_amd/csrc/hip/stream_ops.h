@@ -99,61 +99,80 @@ extern "C" __global__ __launch_bounds__(MXK_BLOCK) void mx_chan_scale_s(ChanScal
 
 // ------------------------------------------------------------ LayerNorm
 //
-// One thread owns V adjacent pixels and holds their C channel values in
-// registers, so x is read once. Per pixel: s1, s2 in ascending channel order,
-// m = s1/c, var = s2/c - m*m, r = 1/sqrt(max(var, 0) + eps),
-// y = (x - m) * r * w + b (src/exec_cpu.rs:392-432).
+// Per pixel: s1, s2 in ascending channel order, m = s1/c, var = s2/c - m*m,
+// r = 1/sqrt(max(var, 0) + eps), y = (x - m) * r * w + b
+// (src/exec_cpu.rs:392-432) - the same operations in the same order, so the
+// result is the CPU path's to the bit.
+//
+// A block owns P adjacent pixels: all 256 threads stage the [C][P] tile in
+// LDS with 128-bit loads (every channel row is P contiguous floats), then P
+// threads run the serial channel sums out of LDS, then all 256 threads
+// normalise and store. The staging is what keeps many loads in flight; the
+// serial part runs at LDS latency, not memory latency.
 
-template <int C, int V>
-__device__ void chan_ln_body(const ChanLnArgs &a) {
-    const int64_t p0 = ((int64_t)blockIdx.x * MXK_BLOCK + threadIdx.x) * V;
-    if (p0 >= a.hw) return;
-    float v[C][V];
-    float s1[V], s2[V];
-#pragma unroll
-    for (int k = 0; k < V; ++k) { s1[k] = 0.0f; s2[k] = 0.0f; }
-#pragma unroll
-    for (int c = 0; c < C; ++c) {
-        const float *row = a.x + (int64_t)c * a.hw + p0;
-        if (V == 4) {
-            float4 q = ld4(row);
-            v[c][0] = q.x; v[c][1 % V] = q.y; v[c][2 % V] = q.z; v[c][3 % V] = q.w;
-        } else if (V == 2) {
-            float2 q = *reinterpret_cast<const float2 *>(row);
-            v[c][0] = q.x; v[c][1 % V] = q.y;
+template <int C, int P>
+__device__ void chan_ln_tile(const ChanLnArgs &a) {
+    static_assert(C * P == 8192, "a 32 KiB tile");
+    __shared__ float t[C][P];
+    __shared__ float st[2][P];
+    const int tid = threadIdx.x;
+    const int64_t p0 = (int64_t)blockIdx.x * P;
+    const bool full = p0 + P <= a.hw;
+    constexpr int Q = P / 4;  // float4s per channel row
+    for (int i = tid; i < C * Q; i += MXK_BLOCK) {
+        const int c = i / Q, q = (i % Q) * 4;
+        const float *src = a.x + (int64_t)c * a.hw + p0 + q;
+        float4 v;
+        if (full) {
+            v = ld4(src);
         } else {
-            v[c][0] = row[0];
+            v.x = p0 + q < a.hw ? src[0] : 0.0f;
+            v.y = p0 + q + 1 < a.hw ? src[1] : 0.0f;
+            v.z = p0 + q + 2 < a.hw ? src[2] : 0.0f;
+            v.w = p0 + q + 3 < a.hw ? src[3] : 0.0f;
         }
-#pragma unroll
-        for (int k = 0; k < V; ++k) {
-            s1[k] += v[c][k];
-            s2[k] += v[c][k] * v[c][k];
+        st4(&t[c][q], v);
+    }
+    __syncthreads();
+    if (tid < P) {
+        float s1 = 0.0f, s2 = 0.0f;
+#pragma unroll 8
+        for (int c = 0; c < C; ++c) {
+            const float v = t[c][tid];
+            s1 += v;
+            s2 += v * v;
         }
+        const float nf = (float)C;
+        const float m = s1 / nf;
+        const float var = s2 / nf - m * m;
+        st[0][tid] = m;
+        st[1][tid] = 1.0f / sqrtf(fmaxf(var, 0.0f) + a.eps);
     }
-    const float nf = (float)C;
-    float m[V], r[V];
-#pragma unroll
-    for (int k = 0; k < V; ++k) {
-        m[k] = s1[k] / nf;
-        float var = s2[k] / nf - m[k] * m[k];
-        r[k] = 1.0f / sqrtf(fmaxf(var, 0.0f) + a.eps);
-    }
-#pragma unroll
-    for (int c = 0; c < C; ++c) {
+    __syncthreads();
+    for (int i = tid; i < C * Q; i += MXK_BLOCK) {
+        const int c = i / Q, q = (i % Q) * 4;
         const float w = a.scale[c], b = a.bias[c];
-        float o[V];
-#pragma unroll
-        for (int k = 0; k < V; ++k) o[k] = (v[c][k] - m[k]) * r[k] * w + b;
-        float *row = a.y + (int64_t)c * a.hw + p0;
-        if (V == 4) st4(row, make_float4(o[0], o[1 % V], o[2 % V], o[3 % V]));
-        else if (V == 2) *reinterpret_cast<float2 *>(row) = make_float2(o[0], o[1 % V]);
-        else row[0] = o[0];
+        float4 v = ld4(&t[c][q]);
+        v.x = (v.x - st[0][q]) * st[1][q] * w + b;
+        v.y = (v.y - st[0][q + 1]) * st[1][q + 1] * w + b;
+        v.z = (v.z - st[0][q + 2]) * st[1][q + 2] * w + b;
+        v.w = (v.w - st[0][q + 3]) * st[1][q + 3] * w + b;
+        float *dst = a.y + (int64_t)c * a.hw + p0 + q;
+        if (full) {
+            st4(dst, v);
+        } else {
+            if (p0 + q < a.hw) dst[0] = v.x;
+            if (p0 + q + 1 < a.hw) dst[1] = v.y;
+            if (p0 + q + 2 < a.hw) dst[2] = v.z;
+            if (p0 + q + 3 < a.hw) dst[3] = v.w;
+        }
     }
 }
 
-extern "C" __global__ __launch_bounds__(MXK_BLOCK) void mx_chan_ln_c32(ChanLnArgs a) { chan_ln_body<32, 4>(a); }
-extern "C" __global__ __launch_bounds__(MXK_BLOCK) void mx_chan_ln_c64(ChanLnArgs a) { chan_ln_body<64, 2>(a); }
-extern "C" __global__ __launch_bounds__(MXK_BLOCK) void mx_chan_ln_c128(ChanLnArgs a) { chan_ln_body<128, 1>(a); }
+// 128-bit paths need hw % 4 == 0 and 16-byte aligned x and y.
+extern "C" __global__ __launch_bounds__(MXK_BLOCK) void mx_chan_ln_c32(ChanLnArgs a) { chan_ln_tile<32, 256>(a); }
+extern "C" __global__ __launch_bounds__(MXK_BLOCK) void mx_chan_ln_c64(ChanLnArgs a) { chan_ln_tile<64, 128>(a); }
+extern "C" __global__ __launch_bounds__(MXK_BLOCK) void mx_chan_ln_c128(ChanLnArgs a) { chan_ln_tile<128, 64>(a); }
 
 // Any channel count, any alignment: reads x twice.
 extern "C" __global__ __launch_bounds__(MXK_BLOCK) void mx_chan_ln_any(ChanLnArgs a) {
