@@ -48,15 +48,45 @@ int mxh_run(mxh_gpu *g, const mx_plan_desc *plan, const float *input, uint64_t n
 int mxh_begin(mxh_gpu *g, const mx_plan_desc *plan, const float *input, uint64_t n_in);
 /* Gpu::step_op (src/exec_gpu.rs:346-351): execute exactly op `i`. */
 int mxh_step_op(mxh_gpu *g, const mx_plan_desc *plan, uint64_t i);
+/* Every op over the image already in the arena as ONE captured HIP graph
+ * (captured on the first call, replayed after), asynchronously. The graph
+ * launches exactly the kernels mxh_run_ops would, in the same order. */
+int mxh_run_graph(mxh_gpu *g, const mx_plan_desc *plan);
+/* Make mxh_run replay the captured graph instead of launching op by op. */
+void mxh_set_graph(mxh_gpu *g, int on);
+/* Fusion (on by default) runs mxh_run / mxh_run_ops / mxh_run_graph through
+ * the fused program: a producer whose output has one reader applies that
+ * reader in its epilogue (GEMM + GELU, GEMM + residual add(s), gate Dense +
+ * gate multiply, GEMM into a concatenation slot, 3x3 conv + leaky ReLU). The
+ * fused epilogue performs the same float operations in the same order, so
+ * results are bitwise those of the unfused launches. mxh_step_op never fuses. */
+void mxh_set_fusion(mxh_gpu *g, int on);
+/* The same decisions without a device: how many ops fuse away, the device
+ * arena length and every buffer's device offset (n_bufs entries), and the
+ * steps' op ranges (room for n_ops entries each). `repack` = 0 keeps the
+ * plan's own layout. */
+int mxh_plan_program(const mx_plan_desc *plan, int repack, uint64_t *fused_ops, uint64_t *arena_len,
+                     uint64_t *offs, uint64_t *step_first, uint64_t *step_last, uint64_t *n_steps);
+uint64_t mxh_fused_ops(mxh_gpu *g);
+uint64_t mxh_steps(mxh_gpu *g);
+int mxh_step_info(mxh_gpu *g, uint64_t i, uint64_t *first, uint64_t *last, const char **kernel);
 /* All ops [first, last) in order, asynchronously (no host synchronisation). */
 int mxh_run_ops(mxh_gpu *g, const mx_plan_desc *plan, uint64_t first, uint64_t last);
 /* Gpu::read_buf (src/exec_gpu.rs:353-357): one buffer back to the host. */
 int mxh_read_buf(mxh_gpu *g, const mx_plan_desc *plan, uint64_t buf, float *out, uint64_t n);
-/* Gpu::read_into / read_arena (src/exec_gpu.rs:285-300): `n` floats from arena element `off`. */
+/* One buffer from the host (Gpu::write_at, src/exec_gpu.rs:272-281, by
+ * buffer id): the per-op parity walk uses it to give an op exactly the CPU
+ * path's inputs. */
+int mxh_write_buf(mxh_gpu *g, const mx_plan_desc *plan, uint64_t buf, const float *in, uint64_t n);
+/* The device arena: where buffer `buf` lives in it (elements). This is the
+ * plan's own offset unless the executor laid the arena out by fused steps
+ * (the plan supplied its view table); mxh_arena_bytes is its size. */
+uint64_t mxh_buf_offset(mxh_gpu *g, uint64_t buf);
+/* Gpu::read_into / read_arena (src/exec_gpu.rs:285-300): `n` floats from
+ * device-arena element `off` (mxh_buf_offset), and the whole device arena. */
 int mxh_read_into(mxh_gpu *g, uint64_t off, float *out, uint64_t n);
 int mxh_read_arena(mxh_gpu *g, float *out, uint64_t n);
-/* The inverse of mxh_read_into (Gpu::write_at, src/exec_gpu.rs:272-281): used
- * by the per-op parity walk to give an op exactly the CPU path's inputs. */
+/* `n` floats to device-arena element `off`. */
 int mxh_write_into(mxh_gpu *g, uint64_t off, const float *in, uint64_t n);
 /* MAXIM_POISON (src/exec_gpu.rs:313-340): fill the whole arena with 0xCD bytes. */
 int mxh_poison(mxh_gpu *g);
@@ -64,10 +94,12 @@ int mxh_poison(mxh_gpu *g);
 int mxh_sync(mxh_gpu *g);
 
 /* Gpu::set_timeline / timeline (src/exec_gpu.rs:176-194, 231-265): with the
- * timeline on, mxh_run records one HIP event per op and reports per-op device
- * milliseconds, synchronising once at the end. */
+ * timeline on, mxh_run records one HIP event per step and reports per-step
+ * device milliseconds, synchronising once at the end. A step is one op, or -
+ * with fusion on - one fused launch standing for several ops (mxh_step_info);
+ * with fusion off there is one step per op. */
 void mxh_set_timeline(mxh_gpu *g, int on);
-int mxh_timeline(mxh_gpu *g, float *per_op_ms, uint64_t n, float *total_ms);
+int mxh_timeline(mxh_gpu *g, float *per_step_ms, uint64_t n, float *total_ms);
 /* Gpu::run_timed (src/exec_gpu.rs:241-265) without the copies: every op over
  * the image already in the arena, one event per op, one synchronisation. */
 int mxh_run_timed(mxh_gpu *g, const mx_plan_desc *plan);

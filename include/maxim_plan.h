@@ -110,6 +110,15 @@ typedef struct mx_plan_desc {
     const uint64_t *weight_lens;   /* elements per blob */
     uint64_t arena_len;            /* elements */
     uint64_t input, output;        /* buffer ids */
+    /* Optional (NULL when the host does not have them): the view table -
+     * alias_parent[b] is the buffer whose channels `b` is a range of, or -1,
+     * and alias_delta[b] the element offset into it (Plan::alias,
+     * src/model.rs:1265-1271) - and keep[b] != 0 for buffers that must stay
+     * intact to the end of a pass (the named dumps). With them, an executor
+     * may lay its device arena out itself; without them it uses `offs`. */
+    const int64_t *alias_parent;
+    const uint64_t *alias_delta;
+    const uint8_t *keep;
 } mx_plan_desc;
 
 /* The model geometry (src/config.rs:8-59). */

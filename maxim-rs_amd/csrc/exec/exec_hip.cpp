@@ -42,6 +42,14 @@ struct Launch {
     alignas(16) unsigned char a0[128];
     alignas(16) unsigned char a1[32];
     int nparams = 1;
+    int kind = 0;  // 1: a0 holds GemmArgs (plain epilogue), 2: ConvArgs
+};
+
+// A run of ops [first, last) executed by `launches`: one op's own launches,
+// or one fused launch standing for several ops.
+struct Step {
+    uint64_t first, last;
+    std::vector<Launch> launches;
 };
 
 template <typename T>
@@ -191,6 +199,25 @@ std::string conv_name(ConvCfg c, bool k3) {
 
 }  // namespace
 
+// What the executor decides about a plan before touching the device: which
+// ops fuse into which steps, and where every buffer lives in the device arena.
+struct StepSpec {
+    uint64_t first = 0, last = 0;
+    int64_t out = -1, u = -1, r1 = -1, r2 = -1;
+    int act = MXK_ACT_NONE;
+    float slope = 0.0f;
+};
+
+struct Program {
+    std::vector<StepSpec> specs;
+    std::vector<uint64_t> doff;  // device element offset of every buffer
+    uint64_t arena_len = 0;
+    uint64_t fused_ops = 0;
+    bool repacked = false;
+    void plan_fusion(const mx_plan_desc *p, bool require_clear);
+    void layout(const mx_plan_desc *p, bool repack);
+};
+
 class Gpu {
 public:
     explicit Gpu(const mx_plan_desc *p);
@@ -214,9 +241,39 @@ public:
     bool have_timeline = false;
     std::string name;
     int cus = 0, clock_khz = 0;
+    bool use_graph = false;
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t gexec = nullptr;
+
+    // The whole op list as one captured graph, instantiated on first use and
+    // replayed after: one submission per pass instead of one per kernel.
+    void run_graph() {
+        if (!gexec) {
+            check(H.hipStreamBeginCapture(stream, kCaptureModeThreadLocal), "hipStreamBeginCapture");
+            const uint64_t l0 = launched, k0 = kernels;
+            try {
+                if (fusion) run_range(0, n_ops);
+                else for (uint64_t i = 0; i < n_ops; ++i) run_op(i);
+            } catch (...) {
+                hipGraph_t g = nullptr;
+                H.hipStreamEndCapture(stream, &g);
+                if (g) H.hipGraphDestroy(g);
+                throw;
+            }
+            launched = l0;
+            graph_kernels = kernels - k0;
+            kernels = k0;
+            check(H.hipStreamEndCapture(stream, &graph), "hipStreamEndCapture");
+            check(H.hipGraphInstantiate(&gexec, graph, nullptr, nullptr, 0), "hipGraphInstantiate");
+        }
+        check(H.hipGraphLaunch(gexec, stream), "hipGraphLaunch");
+        launched += n_ops;
+        kernels += graph_kernels;
+    }
+    uint64_t graph_kernels = 0;
 
     void check_plan(const mx_plan_desc *p) const {
-        if (p->n_ops != n_ops || p->n_bufs != n_bufs || p->arena_len != arena_len)
+        if (p->n_ops != n_ops || p->n_bufs != n_bufs || p->arena_len != plan_arena_len)
             throw Error("this executor was built for a different plan");
     }
     void launch(Launch &l) {
@@ -230,14 +287,37 @@ public:
         for (auto &l : ops[i]) launch(l);
         ++launched;
     }
+    // Ops [first, last) through the fused program; a step that straddles the
+    // range runs its ops one by one.
+    void run_range(uint64_t first, uint64_t last) {
+        for (const Step &st : prog) {
+            if (st.last <= first || st.first >= last) continue;
+            if (st.first >= first && st.last <= last) {
+                for (auto &l : st.launches) launch(const_cast<Launch &>(l));
+                launched += st.last - st.first;
+            } else {
+                for (uint64_t i = std::max(first, st.first); i < std::min(last, st.last); ++i) run_op(i);
+            }
+        }
+    }
+    std::vector<Step> prog;
+    bool fusion = true;
+    Program pg;                   // the fusion decisions and the device layout
+    std::vector<uint64_t> &doff;  // = pg.doff
+    uint64_t plan_arena_len = 0;
+    void build_program(const mx_plan_desc *p);
     void sync() { check(H.hipStreamSynchronize(stream), "hipStreamSynchronize"); }
     // All ops with an event before each and one after the last; one sync.
-    void run_timed(uint64_t n) {
+    // Every step (one op, or one fused launch standing for several) with an
+    // event before each and one after the last; one synchronisation.
+    void run_timed() {
+        const uint64_t n = fusion ? prog.size() : n_ops;
         std::vector<hipEvent_t> ev(n + 1);
         for (auto &e : ev) check(H.hipEventCreate(&e), "hipEventCreate");
         for (uint64_t i = 0; i < n; ++i) {
             check(H.hipEventRecord(ev[i], stream), "hipEventRecord");
-            run_op(i);
+            if (fusion) run_range(prog[i].first, prog[i].last);
+            else run_op(i);
         }
         check(H.hipEventRecord(ev[n], stream), "hipEventRecord");
         sync();
@@ -397,7 +477,7 @@ void Gpu::validate(const mx_plan_desc *p) const {
     }
 }
 
-Gpu::Gpu(const mx_plan_desc *p) : H(hip()) {
+Gpu::Gpu(const mx_plan_desc *p) : H(hip()), doff(pg.doff) {
     validate(p);
     check(H.hipInit(0), "hipInit");
     int ndev = 0;
@@ -506,10 +586,16 @@ Gpu::Gpu(const mx_plan_desc *p) : H(hip()) {
     }
     blob.resize((blob.size() + 63) & ~(size_t)63);
 
-    // Size the pass before allocating it, and refuse with the numbers.
-    arena_len = p->arena_len;
+    // The fused program and the device layout it implies.
     n_ops = p->n_ops;
     n_bufs = p->n_bufs;
+    plan_arena_len = p->arena_len;
+    const bool repack = p->alias_parent && p->alias_delta && !std::getenv("MAXIM_PLAN_LAYOUT");
+    pg.plan_fusion(p, !repack);
+    pg.layout(p, repack);
+    arena_len = pg.arena_len;
+
+    // Size the pass before allocating it, and refuse with the numbers.
     wbytes = blob.size() * 4;
     scratch_len = std::max<uint64_t>(mean_scratch, 64);
     const uint64_t need = arena_len * 4 + wbytes + scratch_len * 4;
@@ -519,7 +605,7 @@ Gpu::Gpu(const mx_plan_desc *p) : H(hip()) {
                     std::to_string(p->bufs[p->input].h) + " pass\nmaxim: the arena needs " +
                     std::to_string((arena_len * 4) >> 20) + " MiB and the weights " + std::to_string(wbytes >> 20) +
                     " MiB; " + std::to_string(free_b >> 20) +
-                    " MiB is free\nmaxim: the arena is exact - it is the plan's own packed size - so this is a hard limit");
+                    " MiB is free\nmaxim: the arena is exact - the packed size of this pass - so this is a hard limit");
     }
     void *ptr = nullptr;
     hipError_t rc = H.hipMalloc(&ptr, std::max<uint64_t>(arena_len, 1) * 4);
@@ -534,12 +620,13 @@ Gpu::Gpu(const mx_plan_desc *p) : H(hip()) {
     if (wbytes) check(H.hipMemcpy(wdev, blob.data(), wbytes, kMemcpyH2D), "hipMemcpy(weights)");
 
     build_launches(p, woff, extra, maxt);
+    build_program(p);
 }
 
 void Gpu::build_launches(const mx_plan_desc *p, const std::vector<int64_t> &woff,
                          const std::vector<std::array<int64_t, 4>> &extra,
                          const std::vector<std::array<int, 2>> &maxt) {
-    auto B = [&](int64_t id) { return arena + p->offs[id]; };
+    auto B = [&](int64_t id) { return arena + doff[id]; };
     auto W = [&](int64_t id) -> const float * {
         return id >= 0 ? reinterpret_cast<const float *>(wdev) + woff[id] : nullptr;
     };
@@ -646,11 +733,13 @@ void Gpu::build_launches(const mx_plan_desc *p, const std::vector<int64_t> &woff
                 a.bias_mode = o.bias >= 0 ? MXK_BIAS_ROW : MXK_BIAS_NONE;
                 a.epi = MXK_EPI_PLAIN;
                 if (plane > 0x7fffffff) throw Error("conv1x1 plane too large");
+                a.cvec = aligned(a.C, 16) && plane % 4 == 0;
                 Tile t = pick_tile(o.c_out, plane, 1, cus);
                 Launch l = mk(gemm_name(t, o.c_in % 4 == 0 && aligned(a.A, 16)));
                 l.g[0] = cdiv(plane, t.bn);
                 l.g[1] = grid_yz((o.c_out + t.bm - 1) / t.bm);
                 set_args(l, a);
+                l.kind = 1;
                 L.push_back(l);
                 break;
             }
@@ -670,12 +759,14 @@ void Gpu::build_launches(const mx_plan_desc *p, const std::vector<int64_t> &woff
                 a.ow = (int32_t)(k3 ? o.wd : o.ow);
                 a.pad_top = (int32_t)(k3 ? 1 : o.p[0]);
                 a.pad_left = (int32_t)(k3 ? 1 : o.p[1]);
+                a.cvec = aligned(a.y, 16) && a.ow % 4 == 0;
                 const ConvCfg &cc = ccfg[i];
                 Launch l = mk(conv_name(cc, k3));
                 const int64_t tiles = (int64_t)((a.oh + cc.th - 1) / cc.th) * ((a.ow + 15) / 16);
                 l.g[0] = cdiv(tiles, 1);
                 l.g[1] = grid_yz((o.c_out + cc.bm - 1) / cc.bm);
                 set_args(l, a);
+                l.kind = 2;
                 L.push_back(l);
                 break;
             }
@@ -695,7 +786,7 @@ void Gpu::build_launches(const mx_plan_desc *p, const std::vector<int64_t> &woff
                 a.co = (int32_t)o.c_out;
                 a.wd = (int32_t)o.wd;
                 Tile t = pick_tile(a.M, plane, 1, cus);
-                Launch l = mk(gemm_name(t, o.c_in % 4 == 0 && aligned(a.A, 16)));
+                Launch l = mk(gemm_name(t, o.c_in % 4 == 0 && aligned(a.A, 16)) + "_t");
                 l.g[0] = cdiv(plane, t.bn);
                 l.g[1] = grid_yz((a.M + t.bm - 1) / t.bm);
                 set_args(l, a);
@@ -719,12 +810,14 @@ void Gpu::build_launches(const mx_plan_desc *p, const std::vector<int64_t> &woff
                     a.N = (int32_t)inner;
                     a.batch = (int32_t)o.c;
                     a.bias_mode = o.bias >= 0 ? MXK_BIAS_ROW : MXK_BIAS_NONE;
+                    a.cvec = aligned(a.C, 16) && inner % 4 == 0 && a.sC % 4 == 0;
                     Tile t = pick_tile(outer, inner, o.c, cus);
                     Launch l = mk(gemm_name(t, outer % 4 == 0 && aligned(a.A, 16)));
                     l.g[0] = cdiv(inner, t.bn);
                     l.g[1] = grid_yz((outer + t.bm - 1) / t.bm);
                     l.g[2] = grid_yz(o.c);
                     set_args(l, a);
+                    l.kind = 1;
                     L.push_back(l);
                 } else {
                     // all channels at once: Y = X . W^T, bias by column
@@ -736,11 +829,13 @@ void Gpu::build_launches(const mx_plan_desc *p, const std::vector<int64_t> &woff
                     a.batch = 1;
                     a.bias_mode = o.bias >= 0 ? MXK_BIAS_COL : MXK_BIAS_NONE;
                     if (o.c * outer > 0x7fffffff) throw Error("gate_mm rows too many");
+                    a.cvec = aligned(a.C, 16) && inner % 4 == 0;
                     Tile t = pick_tile(a.M, inner, 1, cus);
                     Launch l = mk(gemm_name(t, inner % 4 == 0 && aligned(a.A, 16)));
                     l.g[0] = cdiv(inner, t.bn);
                     l.g[1] = grid_yz((a.M + t.bm - 1) / t.bm);
                     set_args(l, a);
+                    l.kind = 1;
                     L.push_back(l);
                 }
                 break;
@@ -813,8 +908,260 @@ void Gpu::build_launches(const mx_plan_desc *p, const std::vector<int64_t> &woff
     }
 }
 
+// The fused program. Each rule replaces an op whose output has exactly one
+// reader with one launch that applies the reader in the producer's epilogue
+// (see Epilogue in kargs.h: the same operations in the same order, so fused
+// and unfused passes agree to the bit):
+//   GEMM -> Gelu                       (every in-projection / MLP Dense)
+//   GEMM -> Add [-> Add]               (out-projections + residuals)
+//   GateMm -> GateApply                (the gMLP gate, u * (Dense(v) + 1))
+//   GEMM -> Copy                       (a Dense written straight into its
+//                                       slot of a channel concatenation)
+//   Conv3x3 -> Lrelu                   (RCAB)
+// "Exactly one reader" is decided on the plan's own arena: the bytes of the
+// intermediate stay live until later writes have covered them all, and no op
+// but the consumer may read a live byte in that window. With the plan's view
+// table the executor then lays out its own device arena by steps (below), so
+// a fused step's operands can never overlap; without it the plan layout is
+// kept and a pair only fuses where its output overlaps nothing it reads.
+void Program::plan_fusion(const mx_plan_desc *p, bool require_clear) {
+    struct R {
+        uint64_t a, b;
+    };
+    auto range = [&](int64_t id) -> R {
+        const mx_bufshape &s = p->bufs[id];
+        return R{p->offs[id], p->offs[id] + (uint64_t)(s.c * s.h * s.w)};
+    };
+    auto overlap = [](R x, R y) { return x.a < y.b && y.a < x.b; };
+    auto reads_of = [&](const mx_op &o) {
+        std::vector<int64_t> v{o.src};
+        if (o.src2 >= 0 && o.kind != MX_OP_RESIZE) v.push_back(o.src2);
+        return v;
+    };
+    auto writes_of = [&](const mx_op &o) {
+        std::vector<int64_t> v{o.dst};
+        if (o.kind == MX_OP_RESIZE) v.push_back(o.src2);  // the tmp, written before it is read
+        return v;
+    };
+    auto only_reader = [&](int64_t x, uint64_t i, uint64_t j) {
+        std::vector<R> live{range(x)};
+        for (uint64_t k = i + 1; k < p->n_ops && !live.empty(); ++k) {
+            const mx_op &o = p->ops[k];
+            if (k != j)
+                for (int64_t s : reads_of(o))
+                    for (const R &l : live)
+                        if (overlap(range(s), l)) return false;
+            for (int64_t d : writes_of(o)) {
+                const R w = range(d);
+                std::vector<R> rest;
+                for (const R &l : live) {
+                    if (!overlap(w, l)) { rest.push_back(l); continue; }
+                    if (l.a < w.a) rest.push_back(R{l.a, w.a});
+                    if (w.b < l.b) rest.push_back(R{w.b, l.b});
+                }
+                live.swap(rest);
+            }
+        }
+        return true;
+    };
+    auto whole = [&](const mx_op &o, int64_t x) { return o.n == (int64_t)(range(x).b - range(x).a); };
+    auto gemm_op = [&](const mx_op &o) {
+        return (o.kind == MX_OP_CONV1X1 && o.h * o.wd > 1) || o.kind == MX_OP_GATE_MM;
+    };
+    auto clear_of = [&](int64_t dst, const std::vector<int64_t> &reads) {
+        if (!require_clear) return true;
+        for (int64_t r : reads)
+            if (overlap(range(dst), range(r))) return false;
+        return true;
+    };
+
+    specs.clear();
+    fused_ops = 0;
+    for (uint64_t i = 0; i < p->n_ops;) {
+        const mx_op &o = p->ops[i];
+        StepSpec sp;
+        sp.first = i;
+        sp.last = i + 1;
+        if (i + 1 < p->n_ops && (gemm_op(o) || o.kind == MX_OP_CONV3X3) && only_reader(o.dst, i, i + 1)) {
+            const int64_t x = o.dst;
+            const mx_op &n1 = p->ops[i + 1];
+            std::vector<int64_t> reads = reads_of(o);
+            StepSpec f = sp;
+            if (o.kind == MX_OP_GATE_MM && n1.kind == MX_OP_GATE_APPLY && n1.src2 == x && n1.src != x &&
+                whole(n1, x)) {
+                f.u = n1.src;
+                f.out = n1.dst;
+                f.last = i + 2;
+            } else if (o.kind == MX_OP_CONV1X1 && n1.kind == MX_OP_GELU && n1.src == x && whole(n1, x)) {
+                f.act = MXK_ACT_GELU;
+                f.out = n1.dst;
+                f.last = i + 2;
+            } else if (o.kind == MX_OP_CONV3X3 && n1.kind == MX_OP_LRELU && n1.src == x && whole(n1, x)) {
+                f.act = MXK_ACT_LRELU;
+                f.slope = n1.slope;
+                f.out = n1.dst;
+                f.last = i + 2;
+            } else if (o.kind == MX_OP_CONV1X1 && n1.kind == MX_OP_COPY && n1.src == x && whole(n1, x)) {
+                f.out = n1.dst;
+                f.last = i + 2;
+            } else if (o.kind == MX_OP_CONV1X1 && n1.kind == MX_OP_ADD && (n1.src == x) != (n1.src2 == x) &&
+                       whole(n1, x)) {
+                f.r1 = n1.src == x ? n1.src2 : n1.src;
+                f.out = n1.dst;
+                f.last = i + 2;
+                if (i + 2 < p->n_ops) {
+                    const mx_op &n2 = p->ops[i + 2];
+                    const int64_t y = f.out;
+                    if (n2.kind == MX_OP_ADD && (n2.src == y) != (n2.src2 == y) && whole(n2, y) &&
+                        only_reader(y, i + 1, i + 2)) {
+                        const int64_t r2 = n2.src == y ? n2.src2 : n2.src;
+                        if (clear_of(n2.dst, {f.r1, r2, y})) {
+                            f.r2 = r2;
+                            f.out = n2.dst;
+                            f.last = i + 3;
+                        }
+                    }
+                }
+            }
+            if (f.out >= 0) {
+                for (int64_t r : {f.u, f.r1, f.r2})
+                    if (r >= 0) reads.push_back(r);
+                if (clear_of(f.out, reads)) sp = f;
+            }
+        }
+        fused_ops += sp.last - sp.first - 1;
+        specs.push_back(sp);
+        i = sp.last;
+    }
+}
+
+// The device arena: the plan's own packing rule (largest first, first use as
+// the tie-break, first fit over {0} u {off + size}, src/model.rs:1091-1234)
+// with live ranges counted in STEPS of the fused program, so every operand of
+// a fused step - the eliminated intermediate included, which the unfused path
+// still writes - is live at once and no two of them share storage. Views keep
+// their delta inside their parent; kept (named) buffers live to the end.
+void Program::layout(const mx_plan_desc *p, bool repack) {
+    const uint64_t n = p->n_bufs;
+    doff.assign(n, 0);
+    if (!repack) {
+        for (uint64_t i = 0; i < n; ++i) doff[i] = p->offs[i];
+        arena_len = p->arena_len;
+        return;
+    }
+    std::vector<int64_t> base(n);
+    std::vector<uint64_t> delta(n);
+    for (uint64_t i = 0; i < n; ++i) {
+        const int64_t par = p->alias_parent[i];
+        if (par < 0) { base[i] = (int64_t)i; delta[i] = 0; }
+        else {
+            if ((uint64_t)par >= i) throw Error("the view table names a later buffer as a parent");
+            base[i] = base[par];
+            delta[i] = delta[par] + p->alias_delta[i];
+        }
+    }
+    const uint64_t DEAD = UINT64_MAX;
+    std::vector<uint64_t> first(n, DEAD), last(n, 0);
+    for (uint64_t s = 0; s < specs.size(); ++s)
+        for (uint64_t k = specs[s].first; k < specs[s].last; ++k) {
+            const mx_op &o = p->ops[k];
+            for (int64_t b : {o.dst, o.src, o.src2}) {
+                if (b < 0) continue;
+                const int64_t r = base[b];
+                if (first[r] == DEAD) first[r] = s;
+                last[r] = std::max(last[r], s);
+            }
+        }
+    if (p->keep)
+        for (uint64_t i = 0; i < n; ++i)
+            if (p->keep[i] && first[base[i]] != DEAD) last[base[i]] = specs.size() - 1;
+    std::vector<int64_t> order;
+    auto len = [&](int64_t b) { return (uint64_t)(p->bufs[b].c * p->bufs[b].h * p->bufs[b].w); };
+    for (uint64_t i = 0; i < n; ++i)
+        if (base[i] == (int64_t)i && first[i] != DEAD) order.push_back((int64_t)i);
+    std::stable_sort(order.begin(), order.end(), [&](int64_t a, int64_t b) {
+        if (len(a) != len(b)) return len(a) > len(b);
+        return first[a] < first[b];
+    });
+    struct Block { uint64_t start, end, off, size; };
+    std::vector<Block> placed;
+    std::vector<uint64_t> off(n, 0), cands;
+    std::vector<const Block *> live;
+    uint64_t total = 0;
+    for (int64_t b : order) {
+        const uint64_t size = len(b), st = first[b], en = last[b];
+        cands.assign(1, 0);
+        live.clear();
+        for (auto &q : placed) {
+            cands.push_back(q.off + q.size);
+            if (st <= q.end && q.start <= en) live.push_back(&q);
+        }
+        std::sort(cands.begin(), cands.end());
+        cands.erase(std::unique(cands.begin(), cands.end()), cands.end());
+        uint64_t chosen = total;
+        for (uint64_t c : cands) {
+            bool clash = false;
+            for (const Block *q : live)
+                if (c < q->off + q->size && q->off < c + size) { clash = true; break; }
+            if (!clash) { chosen = c; break; }
+        }
+        off[b] = chosen;
+        total = std::max(total, chosen + size);
+        placed.push_back({st, en, chosen, size});
+    }
+    for (uint64_t i = 0; i < n; ++i) doff[i] = off[base[i]] + delta[i];
+    arena_len = std::max<uint64_t>(total, 1);
+    repacked = true;
+}
+
+// Materialise the program: single-op steps reuse the op's launches; a fused
+// step is the producer's launch with its destination and epilogue patched.
+void Gpu::build_program(const mx_plan_desc *p) {
+    auto dev = [&](int64_t id) -> float * { return id >= 0 ? arena + doff[id] : nullptr; };
+    prog.clear();
+    for (const StepSpec &sp : pg.specs) {
+        if (sp.out < 0) {
+            prog.push_back(Step{sp.first, sp.last, ops[sp.first]});
+            continue;
+        }
+        Epilogue e{};
+        e.u = dev(sp.u);
+        e.r1 = dev(sp.r1);
+        e.r2 = dev(sp.r2);
+        e.act = sp.act;
+        e.slope = sp.slope;
+        // 128-bit stores need every array the epilogue indexes like the
+        // output on a 16-byte boundary.
+        const bool ealign = aligned(e.u, 16) && aligned(e.r1, 16) && aligned(e.r2, 16);
+        Launch l = ops[sp.first][0];
+        l.name = intern(std::string(l.name) + "_f");
+        l.f = fn(l.name);
+        if (l.kind == 1) {
+            GemmArgs a;
+            memcpy(&a, l.a0, sizeof a);
+            a.C = dev(sp.out);
+            a.e = e;
+            a.cvec = a.N % 4 == 0 && a.sC % 4 == 0 && aligned(a.C, 16) && ealign;
+            set_args(l, a);
+        } else if (l.kind == 2) {
+            ConvArgs a;
+            memcpy(&a, l.a0, sizeof a);
+            a.y = dev(sp.out);
+            a.e = e;
+            a.cvec = a.ow % 4 == 0 && aligned(a.y, 16) && ealign;
+            set_args(l, a);
+        } else {
+            throw Error("internal: a fused step whose producer has no epilogue");
+        }
+        prog.push_back(Step{sp.first, sp.last, {l}});
+    }
+    (void)p;
+}
+
 Gpu::~Gpu() {
     if (stream) H.hipStreamSynchronize(stream);
+    if (gexec) H.hipGraphExecDestroy(gexec);
+    if (graph) H.hipGraphDestroy(graph);
     if (arena) H.hipFree(arena);
     if (wdev) H.hipFree(wdev);
     if (scratch) H.hipFree(scratch);
@@ -877,7 +1224,7 @@ int mxh_begin(mxh_gpu *g, const mx_plan_desc *plan, const float *input, uint64_t
         const mx_bufshape &s = plan->bufs[plan->input];
         if (n_in != (uint64_t)(s.c * s.h * s.w)) throw mx::Error("the input image and the plan's input buffer disagree");
         if (std::getenv("MAXIM_POISON")) mxh::check(G(g)->H.hipMemsetD8Async(G(g)->arena, 0xCD, G(g)->arena_len * 4, G(g)->stream), "poison");
-        G(g)->write(plan->offs[plan->input], input, n_in);
+        G(g)->write(G(g)->doff[plan->input], input, n_in);
     });
 }
 
@@ -894,7 +1241,8 @@ int mxh_run_ops(mxh_gpu *g, const mx_plan_desc *plan, uint64_t first, uint64_t l
     return guard([&] {
         G(g)->check_plan(plan);
         if (last > plan->n_ops || first > last) throw mx::Error("op range out of bounds");
-        for (uint64_t i = first; i < last; ++i) G(g)->run_op(i);
+        if (G(g)->fusion) G(g)->run_range(first, last);
+        else for (uint64_t i = first; i < last; ++i) G(g)->run_op(i);
     });
 }
 
@@ -906,18 +1254,83 @@ int mxh_run(mxh_gpu *g, const mx_plan_desc *plan, const float *input, uint64_t n
         if (n_out != (uint64_t)(so.c * so.h * so.w)) throw mx::Error("the output buffer and the plan's output disagree");
         if (mxh_begin(g, plan, input, n_in) != 0) throw mx::Error(mx_last_error());
         if (x.want_timeline) {
-            x.run_timed(plan->n_ops);
+            x.run_timed();
+        } else if (x.use_graph) {
+            x.run_graph();
         } else {
-            for (uint64_t i = 0; i < plan->n_ops; ++i) x.run_op(i);
+            if (x.fusion) x.run_range(0, plan->n_ops);
+            else for (uint64_t i = 0; i < plan->n_ops; ++i) x.run_op(i);
         }
-        x.read(plan->offs[plan->output], output, n_out);
+        x.read(x.doff[plan->output], output, n_out);
+    });
+}
+
+int mxh_run_graph(mxh_gpu *g, const mx_plan_desc *plan) {
+    return guard([&] {
+        G(g)->check_plan(plan);
+        G(g)->run_graph();
+    });
+}
+
+void mxh_set_graph(mxh_gpu *g, int on) { G(g)->use_graph = on != 0; }
+
+void mxh_set_fusion(mxh_gpu *g, int on) {
+    Gpu &x = *G(g);
+    if (x.fusion != (on != 0) && x.gexec) {
+        // the captured graph holds the other program: capture again on next use
+        x.H.hipGraphExecDestroy(x.gexec);
+        x.H.hipGraphDestroy(x.graph);
+        x.gexec = nullptr;
+        x.graph = nullptr;
+    }
+    x.fusion = on != 0;
+}
+
+int mxh_plan_program(const mx_plan_desc *plan, int repack, uint64_t *fused_ops, uint64_t *arena_len,
+                     uint64_t *offs, uint64_t *step_first, uint64_t *step_last, uint64_t *n_steps) {
+    return guard([&] {
+        mxh::Program pg;
+        const bool rp = repack && plan->alias_parent && plan->alias_delta;
+        pg.plan_fusion(plan, !rp);
+        pg.layout(plan, rp);
+        if (fused_ops) *fused_ops = pg.fused_ops;
+        if (arena_len) *arena_len = pg.arena_len;
+        if (offs) memcpy(offs, pg.doff.data(), sizeof(uint64_t) * pg.doff.size());
+        if (n_steps) *n_steps = pg.specs.size();
+        for (size_t i = 0; i < pg.specs.size(); ++i) {
+            if (step_first) step_first[i] = pg.specs[i].first;
+            if (step_last) step_last[i] = pg.specs[i].last;
+        }
+    });
+}
+
+uint64_t mxh_fused_ops(mxh_gpu *g) { return G(g)->pg.fused_ops; }
+
+uint64_t mxh_steps(mxh_gpu *g) { return G(g)->fusion ? G(g)->prog.size() : G(g)->n_ops; }
+
+int mxh_step_info(mxh_gpu *g, uint64_t i, uint64_t *first, uint64_t *last, const char **kernel) {
+    return guard([&] {
+        Gpu &x = *G(g);
+        if (i >= mxh_steps(g)) throw mx::Error("step index out of range");
+        uint64_t a = i, b = i + 1;
+        const char *k = "";
+        if (x.fusion) {
+            a = x.prog[i].first;
+            b = x.prog[i].last;
+            if (!x.prog[i].launches.empty()) k = x.prog[i].launches[0].name;
+        } else if (!x.ops[i].empty()) {
+            k = x.ops[i][0].name;
+        }
+        if (first) *first = a;
+        if (last) *last = b;
+        if (kernel) *kernel = k;
     });
 }
 
 int mxh_run_timed(mxh_gpu *g, const mx_plan_desc *plan) {
     return guard([&] {
         G(g)->check_plan(plan);
-        G(g)->run_timed(plan->n_ops);
+        G(g)->run_timed();
     });
 }
 
@@ -927,8 +1340,22 @@ int mxh_read_buf(mxh_gpu *g, const mx_plan_desc *plan, uint64_t buf, float *out,
         if (buf >= plan->n_bufs) throw mx::Error("buffer index out of range");
         const mx_bufshape &s = plan->bufs[buf];
         if (n != (uint64_t)(s.c * s.h * s.w)) throw mx::Error("read_buf: wrong length");
-        G(g)->read(plan->offs[buf], out, n);
+        G(g)->read(G(g)->doff[buf], out, n);
     });
+}
+
+int mxh_write_buf(mxh_gpu *g, const mx_plan_desc *plan, uint64_t buf, const float *in, uint64_t n) {
+    return guard([&] {
+        G(g)->check_plan(plan);
+        if (buf >= plan->n_bufs) throw mx::Error("buffer index out of range");
+        const mx_bufshape &s = plan->bufs[buf];
+        if (n != (uint64_t)(s.c * s.h * s.w)) throw mx::Error("write_buf: wrong length");
+        G(g)->write(G(g)->doff[buf], in, n);
+    });
+}
+
+uint64_t mxh_buf_offset(mxh_gpu *g, uint64_t buf) {
+    return buf < G(g)->doff.size() ? G(g)->doff[buf] : UINT64_MAX;
 }
 
 int mxh_read_into(mxh_gpu *g, uint64_t off, float *out, uint64_t n) {

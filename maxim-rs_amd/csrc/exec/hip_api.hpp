@@ -15,9 +15,12 @@ typedef struct ihipStream_t *hipStream_t;
 typedef struct ihipModule_t *hipModule_t;
 typedef struct ihipModuleSymbol_t *hipFunction_t;
 typedef struct ihipEvent_t *hipEvent_t;
+typedef struct ihipGraph *hipGraph_t;
+typedef struct hipGraphExec *hipGraphExec_t;
 
 enum { kMemcpyH2D = 1, kMemcpyD2H = 2, kMemcpyD2D = 3 };
 enum { kAttrClockRate = 5, kAttrMultiprocessorCount = 63 };
+enum { kCaptureModeGlobal = 0, kCaptureModeThreadLocal = 1, kCaptureModeRelaxed = 2 };
 
 struct HipApi {
     void *so = nullptr;

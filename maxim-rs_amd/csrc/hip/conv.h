@@ -18,7 +18,7 @@
 
 namespace conv {
 
-template <int BM, int TH, int TW, int CK, int KS, int STRIDE, int WAVES_M, int WAVES_N>
+template <int BM, int TH, int TW, int CK, int KS, int STRIDE, int WAVES_M, int WAVES_N, bool FUSED>
 __device__ void body(const ConvArgs &a) {
     constexpr int TAPS = KS * KS;
     constexpr int KC = TAPS * CK;
@@ -31,10 +31,13 @@ __device__ void body(const ConvArgs &a) {
     constexpr int NW4 = KC * BM / 4;                // float4s in the weight tile
     constexpr int NW = (NW4 + 255) / 256;           // ... per thread
     constexpr int NH = (HALO + 255) / 256;          // halo elements per thread
-    static_assert(KC % 4 == 0 && BM % 16 == 0, "weight tile");
+    constexpr int LDS = WTN + 4;  // row pitch of a wave's output staging tile
+    constexpr int POOL = KC * LDM + HALO > 4 * 16 * LDS ? KC * LDM + HALO : 4 * 16 * LDS;
+    static_assert(KC % 4 == 0 && BM % 16 == 0 && TW % 4 == 0, "tile");
     static_assert(WAVES_M * WAVES_N == 4 && TM >= 1 && TN >= 1, "wave grid");
-    __shared__ float Ws[KC][LDM];
-    __shared__ float Hs[HALO];
+    __shared__ float smem[POOL];
+    float (*Ws)[LDM] = reinterpret_cast<float (*)[LDM]>(smem);
+    float *Hs = smem + KC * LDM;
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wm = wave / WAVES_N, wn = wave % WAVES_N;
@@ -115,33 +118,66 @@ __device__ void body(const ConvArgs &a) {
         }
     }
 
+    // Stage each 16-channel slab of the wave's tile in LDS and write it out as
+    // rows of four adjacent output pixels per lane.
     const int64_t oplane = (int64_t)a.oh * a.ow;
+    __syncthreads();
+    float *sw = smem + wave * (16 * LDS);
+    constexpr int PER = 16 * WTN / 4 / 64;
+    static_assert(PER * 64 * 4 == 16 * WTN, "slab split");
+    // One float4 at a time through the fused epilogue keeps its registers
+    // (erf and three operand loads per element) from multiplying.
+    constexpr int QU = FUSED ? 1 : PER;
 #pragma unroll
-    for (int j = 0; j < TN; ++j) {
-        const int n = wn * WTN + j * 16 + lr;
-        const int oy = ty0 + n / TW, ox = tx0 + n % TW;
-        if (oy >= a.oh || ox >= a.ow) continue;
+    for (int i = 0; i < TM; ++i) {
 #pragma unroll
-        for (int i = 0; i < TM; ++i) {
+        for (int j = 0; j < TN; ++j)
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int m = m0 + wm * WTM + i * 16 + 4 * lk + r;
-                if (m >= a.co) continue;
-                float v = acc[i][j][r];
-                if (a.bias) v = a.bias[m] + v;
-                a.y[m * oplane + (int64_t)oy * a.ow + ox] = v;
+            for (int r = 0; r < 4; ++r) sw[(4 * lk + r) * LDS + j * 16 + lr] = acc[i][j][r];
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll QU
+        for (int q = 0; q < PER; ++q) {
+            const int e = lane + q * 64;
+            const int row = e / (WTN / 4), c4 = (e % (WTN / 4)) * 4;
+            const int m = m0 + wm * WTM + i * 16 + row;
+            const int n = wn * WTN + c4;
+            const int oy = ty0 + n / TW, ox = tx0 + n % TW;
+            if (m >= a.co || oy >= a.oh || ox >= a.ow) continue;
+            const float4 t = ld4(&sw[row * LDS + c4]);
+            float v[4] = {t.x, t.y, t.z, t.w};
+            const int64_t idx = m * oplane + (int64_t)oy * a.ow + ox;
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                if (a.bias) v[u] = a.bias[m] + v[u];
+                if (FUSED) v[u] = epilogue(a.e, v[u], idx + u);
+            }
+            if (a.cvec && ox + 3 < a.ow) {
+                st4(a.y + idx, make_float4(v[0], v[1], v[2], v[3]));
+            } else {
+#pragma unroll
+                for (int u = 0; u < 4; ++u)
+                    if (ox + u < a.ow) a.y[idx + u] = v[u];
             }
         }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     }
 }
 
 }  // namespace conv
 
-// mx_conv3x3_m<BM>_t<TH>[_c4]: BM output channels x a TH x 16 output tile,
-// CK = 8 input channels per chunk (4 for the _c4 RGB-input forms).
-#define MXK_CONV3(BM, TH, CK, WM, WN, SUF)                                                      \
-    extern "C" __global__ __launch_bounds__(256) void mx_conv3x3_m##BM##_t##TH##SUF(ConvArgs a) { \
-        conv::body<BM, TH, 16, CK, 3, 1, WM, WN>(a);                                            \
+// mx_conv3x3_m<BM>_t<TH>[_c4][_f]: BM output channels x a TH x 16 output
+// tile, CK = 8 input channels per chunk (4 for the _c4 RGB-input forms); _f
+// applies the fused epilogue.
+#define MXK_CONV3(BM, TH, CK, WM, WN, SUF)                                                        \
+    extern "C" __global__ __launch_bounds__(256) void mx_conv3x3_m##BM##_t##TH##SUF(ConvArgs a) {   \
+        conv::body<BM, TH, 16, CK, 3, 1, WM, WN, false>(a);                                       \
+    }                                                                                             \
+    extern "C" __global__ __launch_bounds__(256) void mx_conv3x3_m##BM##_t##TH##SUF##_f(ConvArgs a) { \
+        conv::body<BM, TH, 16, CK, 3, 1, WM, WN, true>(a);                                        \
     }
 MXK_CONV3(32, 8, 8, 1, 4, )
 MXK_CONV3(64, 8, 8, 2, 2, )
@@ -160,7 +196,7 @@ MXK_CONV3(128, 4, 4, 4, 1, _c4)
 // (2 TH + 2) x 34 input halo.
 #define MXK_CONV4(BM, TH, WM, WN)                                                               \
     extern "C" __global__ __launch_bounds__(256) void mx_conv4x4_m##BM##_t##TH(ConvArgs a) {    \
-        conv::body<BM, TH, 16, 4, 4, 2, WM, WN>(a);                                             \
+        conv::body<BM, TH, 16, 4, 4, 2, WM, WN, false>(a);                                      \
     }
 MXK_CONV4(32, 8, 1, 4)
 MXK_CONV4(64, 8, 2, 2)

@@ -90,14 +90,21 @@ struct Stage {
     }
 };
 
-template <int BM, int BN, int WAVES_M, int WAVES_N, bool VEC>
+// Output modes: plain (bias by row or column), fused (bias then the
+// Epilogue), and the transposed-conv scatter.
+enum { PLAIN = 0, FUSED = 1, CONVT = 2 };
+
+template <int BM, int BN, int WAVES_M, int WAVES_N, bool VEC, int MODE>
 __device__ void body(const GemmArgs &a) {
     constexpr int WTM = BM / WAVES_M, WTN = BN / WAVES_N;
     constexpr int TM = WTM / 16, TN = WTN / 16;
+    constexpr int LDS = WTN + 4;  // row pitch of a wave's output staging tile
     static_assert(WAVES_M * WAVES_N == 4, "4 waves");
     static_assert(TM >= 1 && TN >= 1, "wave tile");
-    __shared__ float As[BM][LDK];
-    __shared__ float Bs[BN][LDK];
+    static_assert(4 * 16 * LDS <= (BM + BN) * LDK, "output staging must fit the operand tiles");
+    __shared__ float smem[(BM + BN) * LDK];
+    float (*As)[LDK] = reinterpret_cast<float (*)[LDK]>(smem);
+    float (*Bs)[LDK] = reinterpret_cast<float (*)[LDK]>(smem + BM * LDK);
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wm = wave / WAVES_N, wn = wave % WAVES_N;
@@ -139,47 +146,103 @@ __device__ void body(const GemmArgs &a) {
         }
     }
 
-    // Epilogue: element r of acc[i][j] is row 4*(lane/16) + r, column lane%16.
     float *C = a.C + (int64_t)b * a.sC;
+    if (MODE == CONVT) {
+        // Element r of acc[i][j] is row 4*(lane/16) + r, column lane%16; row
+        // (tap, oc) and column (y, x) scatter to out[oc][2y + ky][2x + kx].
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+            for (int j = 0; j < TN; ++j) {
+                const int n = n0 + wn * WTN + j * 16 + lr;
+                if (n >= N) continue;
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int m = m0 + wm * WTM + i * 16 + 4 * lg + r;
+                    if (m >= M) continue;
+                    const int tap = m / a.co, oc = m - tap * a.co;
+                    const int y = n / a.wd, x = n - y * a.wd;
+                    float v = acc[i][j][r];
+                    if (a.bias) v = a.bias[oc] + v;
+                    C[(int64_t)oc * (4 * (int64_t)N) + (2 * y + (tap >> 1)) * (2 * (int64_t)a.wd) + 2 * x + (tap & 1)] = v;
+                }
+            }
+        return;
+    }
+
+    // Stage each 16-row slab of the wave's tile in LDS (the operand tiles are
+    // free now) and write it out row-contiguous, four columns per lane.
+    __syncthreads();
+    float *sw = smem + wave * (16 * LDS);
+    const bool vec = (N % 4) == 0 && a.cvec;
+    constexpr int PER = 16 * WTN / 4 / 64;  // float4s per lane per slab
+    static_assert(PER * 64 * 4 == 16 * WTN, "slab split");
+    // One float4 at a time through the fused epilogue keeps its registers
+    // (erf and three operand loads per element) from multiplying.
+    constexpr int QU = MODE == FUSED ? 1 : PER;
 #pragma unroll
     for (int i = 0; i < TM; ++i) {
 #pragma unroll
-        for (int j = 0; j < TN; ++j) {
-            const int n = n0 + wn * WTN + j * 16 + lr;
-            if (n >= N) continue;
+        for (int j = 0; j < TN; ++j)
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int m = m0 + wm * WTM + i * 16 + 4 * lg + r;
-                if (m >= M) continue;
-                float v = acc[i][j][r];
-                if (a.epi == MXK_EPI_CONVT) {
-                    const int tap = m / a.co, oc = m - tap * a.co;
-                    const int ky = tap >> 1, kx = tap & 1;
-                    const int y = n / a.wd, x = n - y * a.wd;
-                    const int64_t ow = 2 * (int64_t)a.wd;
-                    if (a.bias) v = a.bias[oc] + v;
-                    C[(int64_t)oc * (4 * (int64_t)N) + (2 * y + ky) * ow + 2 * x + kx] = v;
-                } else {
-                    if (a.bias_mode == MXK_BIAS_ROW) v = a.bias[m] + v;
-                    else if (a.bias_mode == MXK_BIAS_COL) v = a.bias[n] + v;
-                    C[(int64_t)m * N + n] = v;
-                }
+            for (int r = 0; r < 4; ++r) sw[(4 * lg + r) * LDS + j * 16 + lr] = acc[i][j][r];
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll QU
+        for (int q = 0; q < PER; ++q) {
+            const int e = lane + q * 64;
+            const int row = e / (WTN / 4), c4 = (e % (WTN / 4)) * 4;
+            const int m = m0 + wm * WTM + i * 16 + row;
+            const int n = n0 + wn * WTN + c4;
+            if (m >= M || n >= N) continue;
+            float v[4];
+            {
+                const float4 t = ld4(&sw[row * LDS + c4]);
+                v[0] = t.x; v[1] = t.y; v[2] = t.z; v[3] = t.w;
+            }
+            const int64_t row_off = (int64_t)m * N;
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                if (a.bias_mode == MXK_BIAS_ROW) v[t] = a.bias[m] + v[t];
+                else if (a.bias_mode == MXK_BIAS_COL && n + t < N) v[t] = a.bias[n + t] + v[t];
+            }
+            if (MODE == FUSED) {
+                const int64_t base = (int64_t)b * a.sC + row_off + n;
+#pragma unroll
+                for (int t = 0; t < 4; ++t)
+                    if (n + t < N) v[t] = epilogue(a.e, v[t], base + t);
+            }
+            if (vec && n + 3 < N) {
+                st4(C + row_off + n, make_float4(v[0], v[1], v[2], v[3]));
+            } else {
+#pragma unroll
+                for (int t = 0; t < 4; ++t)
+                    if (n + t < N) C[row_off + n + t] = v[t];
             }
         }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     }
 }
 
 }  // namespace gemm
 
-// Entry points: mx_gemm_<BM>x<BN>[_v4]. _v4 reads A with 128-bit loads and
-// needs K % 4 == 0 and A 16-byte aligned; the plain form has no requirement.
-#define MXK_GEMM(BM, BN, WM, WN)                                                                   \
-    extern "C" __global__ __launch_bounds__(256) void mx_gemm_##BM##x##BN(GemmArgs a) {            \
-        gemm::body<BM, BN, WM, WN, false>(a);                                                      \
-    }                                                                                              \
-    extern "C" __global__ __launch_bounds__(256) void mx_gemm_##BM##x##BN##_v4(GemmArgs a) {       \
-        gemm::body<BM, BN, WM, WN, true>(a);                                                       \
+// Entry points: mx_gemm_<BM>x<BN>[_v4][_f|_t]. _v4 reads A with 128-bit loads
+// and needs K % 4 == 0 and A 16-byte aligned; _f applies the fused epilogue,
+// _t is the transposed-conv scatter.
+#define MXK_GEMM1(BM, BN, WM, WN, VEC, MODE, SUF)                                                 \
+    extern "C" __global__ __launch_bounds__(256) void mx_gemm_##BM##x##BN##SUF(GemmArgs a) {      \
+        gemm::body<BM, BN, WM, WN, VEC, gemm::MODE>(a);                                           \
     }
+#define MXK_GEMM(BM, BN, WM, WN)                          \
+    MXK_GEMM1(BM, BN, WM, WN, false, PLAIN, )             \
+    MXK_GEMM1(BM, BN, WM, WN, true, PLAIN, _v4)           \
+    MXK_GEMM1(BM, BN, WM, WN, false, FUSED, _f)           \
+    MXK_GEMM1(BM, BN, WM, WN, true, FUSED, _v4_f)         \
+    MXK_GEMM1(BM, BN, WM, WN, false, CONVT, _t)           \
+    MXK_GEMM1(BM, BN, WM, WN, true, CONVT, _v4_t)
 
 MXK_GEMM(128, 128, 2, 2)
 MXK_GEMM(64, 128, 2, 2)

@@ -83,6 +83,20 @@ struct DownArgs {
 enum { MXK_BIAS_NONE = 0, MXK_BIAS_ROW = 1, MXK_BIAS_COL = 2 };
 enum { MXK_EPI_PLAIN = 0, MXK_EPI_CONVT = 1 };
 
+// A fused epilogue, applied per output element after the bias and in the
+// order of the ops it replaces, so the result is the unfused kernels' to the
+// bit: v = bias + acc; [gate] v = u * (v + 1); [act] v = gelu(v) or lrelu(v);
+// [res1] v = v + r1; [res2] v = v + r2. u, r1, r2 are indexed like C.
+enum { MXK_ACT_NONE = 0, MXK_ACT_GELU = 1, MXK_ACT_LRELU = 2 };
+
+struct Epilogue {
+    const float *u;
+    const float *r1;
+    const float *r2;
+    int32_t act;
+    float slope;
+};
+
 struct GemmArgs {
     const float *A;
     const float *B;
@@ -92,6 +106,8 @@ struct GemmArgs {
     int32_t M, N, K, batch;
     int32_t bias_mode, epi;
     int32_t co, wd;       // convT: output channels and input width
+    int32_t cvec, pad;    // 1: C, u, r1, r2 are 16-byte aligned (128-bit stores)
+    Epilogue e;
 };
 
 // Small GEMV for the plane-1 CALayer convs: y[o] = b[o] + sum_i w[o][i] x[i].
@@ -112,4 +128,6 @@ struct ConvArgs {
     float *y;
     int32_t ci, co, h, wd;
     int32_t oh, ow, pad_top, pad_left;
+    int32_t cvec, pad;    // 1: y, u, r1, r2 are 16-byte aligned and ow % 4 == 0
+    Epilogue e;
 };

@@ -19,7 +19,7 @@ __device__ __forceinline__ float ew1(float a, float b, float slope) {
     if (OP == MXK_ADD) return a + b;
     if (OP == MXK_MUL) return a * b;
     if (OP == MXK_GATE_APPLY) return a * (b + 1.0f);
-    if (OP == MXK_GELU) return 0.5f * a * (1.0f + erff(a * 0.70710678118654752440f));
+    if (OP == MXK_GELU) return gelu_erf(a);
     if (OP == MXK_LRELU) return a >= 0.0f ? a : slope * a;
     return 1.0f / (1.0f + expf(-a));  // MXK_SIGMOID
 }

@@ -123,6 +123,9 @@ void mx_plan_describe(const mx_plan *pp, mx_plan_desc *d) {
     d->arena_len = p->arena_len;
     d->input = (uint64_t)p->input;
     d->output = (uint64_t)p->output;
+    d->alias_parent = p->alias_parent.data();
+    d->alias_delta = p->alias_delta.data();
+    d->keep = p->keep.data();
 }
 
 uint64_t mx_plan_n_dumps(const mx_plan *p) { return reinterpret_cast<const Plan *>(p)->dumps.size(); }

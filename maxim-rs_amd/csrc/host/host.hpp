@@ -98,6 +98,7 @@ struct Plan {
     // Views for mx_plan_describe.
     std::vector<const float *> wptr;
     std::vector<uint64_t> wlen;
+    std::vector<uint8_t> keep;
     void index_weights();
     uint64_t weight_bytes() const;
 };

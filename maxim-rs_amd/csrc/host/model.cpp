@@ -846,6 +846,8 @@ Plan *Builder::finish(int64_t input, int64_t output, BufShape shape) {
     p->labels = std::move(labels_);
     p->alias_parent = std::move(alias_parent_);
     p->alias_delta = std::move(alias_delta_);
+    p->keep.assign(n, 0);
+    for (auto &nm : p->dumps) p->keep[base[nm.second]] = 1;
     p->index_weights();
     return p;
 }

@@ -35,11 +35,20 @@ def _lib():
             "mxh_read_into": (I, [V, U, V, U]),
             "mxh_read_arena": (I, [V, V, U]),
             "mxh_write_into": (I, [V, U, V, U]),
+            "mxh_write_buf": (I, [V, D, U, V, U]),
+            "mxh_buf_offset": (U, [V, U]),
             "mxh_poison": (I, [V]),
             "mxh_sync": (I, [V]),
             "mxh_set_timeline": (None, [V, I]),
             "mxh_timeline": (I, [V, V, U, C.POINTER(C.c_float)]),
             "mxh_run_timed": (I, [V, D]),
+            "mxh_run_graph": (I, [V, D]),
+            "mxh_set_graph": (None, [V, I]),
+            "mxh_set_fusion": (None, [V, I]),
+            "mxh_fused_ops": (U, [V]),
+            "mxh_steps": (U, [V]),
+            "mxh_step_info": (I, [V, U, C.POINTER(C.c_uint64), C.POINTER(C.c_uint64),
+                                  C.POINTER(C.c_char_p)]),
             "mxh_time_ops": (I, [V, D, U, U, I, C.POINTER(C.c_float)]),
             "mxh_device_name": (C.c_char_p, [V]),
             "mxh_arena_bytes": (U, [V]),
@@ -121,10 +130,15 @@ class Gpu:
         _check(_lib().mxh_write_into(self._h, off, d.ctypes.data, d.size))
 
     def write_buf(self, buf, data):
-        self.write_into(int(self.plan.offs[buf]), data)
+        d = np.ascontiguousarray(data, dtype=np.float32)
+        _check(_lib().mxh_write_buf(self._h, self._d, buf, d.ctypes.data, d.size))
+
+    def buf_offset(self, buf):
+        """Where buffer `buf` lives in the device arena (elements)."""
+        return _lib().mxh_buf_offset(self._h, buf)
 
     def read_arena(self):
-        out = np.empty(self.plan.arena_len, np.float32)
+        out = np.empty(self.arena_bytes // 4, np.float32)
         _check(_lib().mxh_read_arena(self._h, out.ctypes.data, out.size))
         return out
 
@@ -137,15 +151,39 @@ class Gpu:
     def set_timeline(self, on=True):
         _lib().mxh_set_timeline(self._h, int(on))
 
+    def set_fusion(self, on=True):
+        _lib().mxh_set_fusion(self._h, int(on))
+
+    @property
+    def fused_ops(self):
+        return _lib().mxh_fused_ops(self._h)
+
+    def steps(self):
+        """[(first op, last op + 1, kernel)] of the program mxh_run executes."""
+        L = _lib()
+        out = []
+        a, b, k = C.c_uint64(), C.c_uint64(), C.c_char_p()
+        for i in range(L.mxh_steps(self._h)):
+            _check(L.mxh_step_info(self._h, i, C.byref(a), C.byref(b), C.byref(k)))
+            out.append((a.value, b.value, k.value.decode()))
+        return out
+
     def timeline(self):
-        n = len(self.plan.ops)
+        n = _lib().mxh_steps(self._h)
         per = np.empty(n, np.float32)
         tot = C.c_float()
         _check(_lib().mxh_timeline(self._h, per.ctypes.data, n, C.byref(tot)))
         return per, tot.value
 
+    def run_graph(self):
+        """Every op over the resident input as one graph replay (asynchronous)."""
+        _check(_lib().mxh_run_graph(self._h, self._d))
+
+    def set_graph(self, on=True):
+        _lib().mxh_set_graph(self._h, int(on))
+
     def run_timed(self):
-        """Every op over the resident input, one event per op: (per-op ms, total ms)."""
+        """Every step over the resident input, one event per step: (per-step ms, total ms)."""
         _check(_lib().mxh_run_timed(self._h, self._d))
         return self.timeline()
 

@@ -62,6 +62,8 @@ class PlanDesc(C.Structure):
         ("n_weights", C.c_uint64), ("weights", C.POINTER(C.POINTER(C.c_float))),
         ("weight_lens", C.POINTER(C.c_uint64)),
         ("arena_len", C.c_uint64), ("input", C.c_uint64), ("output", C.c_uint64),
+        ("alias_parent", C.POINTER(C.c_int64)), ("alias_delta", C.POINTER(C.c_uint64)),
+        ("keep", C.POINTER(C.c_uint8)),
     ]
 
 

@@ -47,8 +47,10 @@ def test_the_code_object_is_embedded_and_complete():
     src = open(os.path.join(ROOT, "maxim-rs_amd", "csrc", "exec", "exec_hip.cpp")).read()
     launched = set(re.findall(r'"(mx_[a-z0-9_]+)"', src))
     launched |= {"mx_gemm_%dx%d%s" % (m, n, v) for m, n in ((128, 128), (64, 128), (128, 64), (64, 64),
-                                                           (32, 128), (32, 64)) for v in ("", "_v4")}
-    launched |= {"mx_conv3x3_m%d_t%d%s" % (m, t, s) for m in (32, 64, 128) for t in (4, 8) for s in ("", "_c4")}
+                                                           (32, 128), (32, 64))
+                 for v in ("", "_v4", "_f", "_v4_f", "_t", "_v4_t")}
+    launched |= {"mx_conv3x3_m%d_t%d%s%s" % (m, t, s, f) for m in (32, 64, 128) for t in (4, 8)
+                 for s in ("", "_c4") for f in ("", "_f")}
     launched |= {"mx_conv4x4_m%d_t%d" % (m, t) for m in (32, 64, 128) for t in (4, 8)}
     launched = {k for k in launched if not k.endswith("_")}
     missing = [k for k in sorted(launched) if k.encode() + b"\0" not in data]
