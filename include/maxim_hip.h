@@ -44,9 +44,9 @@ void mxh_free(mxh_gpu *g);
 /* Gpu::run (src/exec_gpu.rs:196-229): input in, every op, output out. */
 int mxh_run(mxh_gpu *g, const mx_plan_desc *plan, const float *input, uint64_t n_in, float *output,
             uint64_t n_out);
-/* Gpu::begin (src/exec_gpu.rs:313-344): place the input image in the arena. */
+/* Gpu::begin (src/exec_gpu.rs:329-344): place the input image in the arena. */
 int mxh_begin(mxh_gpu *g, const mx_plan_desc *plan, const float *input, uint64_t n_in);
-/* Gpu::step_op (src/exec_gpu.rs:346-351): execute exactly op `i`. */
+/* Gpu::step_op (src/exec_gpu.rs:348-352): execute exactly op `i`. */
 int mxh_step_op(mxh_gpu *g, const mx_plan_desc *plan, uint64_t i);
 /* Every op over the image already in the arena as ONE captured HIP graph
  * (captured on the first call, replayed after), asynchronously. The graph
@@ -72,9 +72,9 @@ uint64_t mxh_steps(mxh_gpu *g);
 int mxh_step_info(mxh_gpu *g, uint64_t i, uint64_t *first, uint64_t *last, const char **kernel);
 /* All ops [first, last) in order, asynchronously (no host synchronisation). */
 int mxh_run_ops(mxh_gpu *g, const mx_plan_desc *plan, uint64_t first, uint64_t last);
-/* Gpu::read_buf (src/exec_gpu.rs:353-357): one buffer back to the host. */
+/* Gpu::read_buf (src/exec_gpu.rs:354-357): one buffer back to the host. */
 int mxh_read_buf(mxh_gpu *g, const mx_plan_desc *plan, uint64_t buf, float *out, uint64_t n);
-/* One buffer from the host (Gpu::write_at, src/exec_gpu.rs:272-281, by
+/* One buffer from the host (Gpu::write_at, src/exec_gpu.rs:275-282, by
  * buffer id): the per-op parity walk uses it to give an op exactly the CPU
  * path's inputs. */
 int mxh_write_buf(mxh_gpu *g, const mx_plan_desc *plan, uint64_t buf, const float *in, uint64_t n);
@@ -82,18 +82,18 @@ int mxh_write_buf(mxh_gpu *g, const mx_plan_desc *plan, uint64_t buf, const floa
  * plan's own offset unless the executor laid the arena out by fused steps
  * (the plan supplied its view table); mxh_arena_bytes is its size. */
 uint64_t mxh_buf_offset(mxh_gpu *g, uint64_t buf);
-/* Gpu::read_into / read_arena (src/exec_gpu.rs:285-300): `n` floats from
+/* Gpu::read_into / read_arena (src/exec_gpu.rs:295-305): `n` floats from
  * device-arena element `off` (mxh_buf_offset), and the whole device arena. */
 int mxh_read_into(mxh_gpu *g, uint64_t off, float *out, uint64_t n);
 int mxh_read_arena(mxh_gpu *g, float *out, uint64_t n);
 /* `n` floats to device-arena element `off`. */
 int mxh_write_into(mxh_gpu *g, uint64_t off, const float *in, uint64_t n);
-/* MAXIM_POISON (src/exec_gpu.rs:313-340): fill the whole arena with 0xCD bytes. */
+/* MAXIM_POISON (src/exec_gpu.rs:320-340): fill the whole arena with 0xCD bytes. */
 int mxh_poison(mxh_gpu *g);
 /* Wait for all queued work. */
 int mxh_sync(mxh_gpu *g);
 
-/* Gpu::set_timeline / timeline (src/exec_gpu.rs:176-194, 231-265): with the
+/* Gpu::set_timeline / timeline (src/exec_gpu.rs:185-194, 241-265): with the
  * timeline on, mxh_run records one HIP event per step and reports per-step
  * device milliseconds, synchronising once at the end. A step is one op, or -
  * with fusion on - one fused launch standing for several ops (mxh_step_info);
@@ -110,7 +110,7 @@ int mxh_time_ops(mxh_gpu *g, const mx_plan_desc *plan, uint64_t first, uint64_t 
                  float *ms);
 
 /* Gpu::device_name / arena_bytes / weight_bytes / pool_bytes / ops_launched
- * (src/exec_gpu.rs:162-175). kernels_launched counts launches (one op may be
+ * (src/exec_gpu.rs:165-183). kernels_launched counts launches (one op may be
  * several, e.g. the two resize passes). */
 const char *mxh_device_name(mxh_gpu *g);
 uint64_t mxh_arena_bytes(mxh_gpu *g);
