@@ -362,6 +362,40 @@ private:
         l.f = fn(l.name);
         return l;
     }
+    // The streaming pointwise kernels (pointwise.h) for a Dense-shaped op,
+    // when its shape and alignment allow them; `layout` 0 = channel-major
+    // output, 1 = row-major. `alt` keeps the tiled-GEMM launch of each op that
+    // got one, for fused steps whose extra operands are not 16-byte aligned.
+    bool try_pw(int layout, const GemmArgs &a, Launch &l) {
+        if (no_pw) return false;
+        const int64_t wout = layout == 0 ? a.M : a.N, slen = layout == 0 ? a.N : a.M;
+        if (a.K % 16 || a.N % 4 || a.K == 0 || wout <= 0 || slen <= 0) return false;
+        if (!aligned(a.A, 16) || !aligned(a.B, 16) || !aligned(a.C, 16)) return false;
+        if (layout == 1 && !aligned(a.bias, 16)) return false;
+        if (a.sA % 4 || a.sB % 4 || a.sC % 4 || a.batch > 65535) return false;
+        static const char *names[2][3] = {{"mx_pw_ch1", "mx_pw_ch2", "mx_pw_ch4"},
+                                          {"mx_pw_rw1", "mx_pw_rw2", "mx_pw_rw4"}};
+        // Tile width and reduction split, from measurements on MI355X: 32
+        // weight outputs per wave except for the long (K >= 256) reductions,
+        // which reuse each operand load over 64; the block's four waves split
+        // reductions of 128 and more, and shorter ones when one wave per tile
+        // would leave SIMDs idle.
+        const int ti = wout <= 16 ? 0 : (wout <= 32 || a.K < 256) ? 1 : 2, tmw = 1 << ti;
+        const int64_t nib = (wout + 16 * tmw - 1) / (16 * tmw);
+        const int64_t tiles = nib * ((slen + 63) / 64);
+        if (tiles > 0x7fffffffLL) return false;
+        const bool k4 = a.K % 64 == 0 && (a.K >= 128 || tiles * a.batch < 2LL * 4 * cus);
+        l = mk(std::string(names[layout][ti]) + (k4 ? "_k4" : ""));
+        const int64_t grid = k4 ? tiles : (tiles + 3) / 4;
+        if (grid > 0x7fffffffLL) return false;
+        l.g[0] = (unsigned)grid;
+        l.g[1] = (unsigned)a.batch;
+        l.kind = 1;
+        set_args(l, a);
+        return true;
+    }
+    std::vector<std::vector<Launch>> alt;
+    bool no_pw = getenv("MAXIM_NO_PW") != nullptr;
     void validate(const mx_plan_desc *p) const;
     void build_launches(const mx_plan_desc *p, const std::vector<int64_t> &woff,
                         const std::vector<std::array<int64_t, 4>> &extra,
@@ -632,6 +666,7 @@ void Gpu::build_launches(const mx_plan_desc *p, const std::vector<int64_t> &woff
     };
     auto X = [&](uint64_t i, int k) { return reinterpret_cast<const float *>(wdev) + extra[i][k]; };
     ops.assign(p->n_ops, {});
+    alt.assign(p->n_ops, {});
     for (uint64_t i = 0; i < p->n_ops; ++i) {
         const mx_op &o = p->ops[i];
         auto &L = ops[i];
@@ -740,7 +775,13 @@ void Gpu::build_launches(const mx_plan_desc *p, const std::vector<int64_t> &woff
                 l.g[1] = grid_yz((o.c_out + t.bm - 1) / t.bm);
                 set_args(l, a);
                 l.kind = 1;
-                L.push_back(l);
+                Launch q;
+                if (try_pw(0, a, q)) {
+                    alt[i].push_back(l);
+                    L.push_back(q);
+                } else {
+                    L.push_back(l);
+                }
                 break;
             }
             case MX_OP_CONV3X3:
@@ -818,7 +859,13 @@ void Gpu::build_launches(const mx_plan_desc *p, const std::vector<int64_t> &woff
                     l.g[2] = grid_yz(o.c);
                     set_args(l, a);
                     l.kind = 1;
-                    L.push_back(l);
+                    Launch q;
+                    if (try_pw(0, a, q)) {
+                        alt[i].push_back(l);
+                        L.push_back(q);
+                    } else {
+                        L.push_back(l);
+                    }
                 } else {
                     // all channels at once: Y = X . W^T, bias by column
                     a.A = B(o.src);
@@ -836,7 +883,17 @@ void Gpu::build_launches(const mx_plan_desc *p, const std::vector<int64_t> &woff
                     l.g[1] = grid_yz((a.M + t.bm - 1) / t.bm);
                     set_args(l, a);
                     l.kind = 1;
-                    L.push_back(l);
+                    // the streaming form reads the Dense kernel [a][t] as is
+                    GemmArgs r = a;
+                    r.A = W(o.w);
+                    r.B = B(o.src);
+                    Launch q;
+                    if (try_pw(1, r, q)) {
+                        alt[i].push_back(l);
+                        L.push_back(q);
+                    } else {
+                        L.push_back(l);
+                    }
                 }
                 break;
             }
@@ -1134,6 +1191,8 @@ void Gpu::build_program(const mx_plan_desc *p) {
         // output on a 16-byte boundary.
         const bool ealign = aligned(e.u, 16) && aligned(e.r1, 16) && aligned(e.r2, 16);
         Launch l = ops[sp.first][0];
+        if (!strncmp(l.name, "mx_pw_", 6) && !(ealign && aligned(dev(sp.out), 16)))
+            l = alt[sp.first][0];  // the streaming kernels store 128 bits at a time
         l.name = intern(std::string(l.name) + "_f");
         l.f = fn(l.name);
         if (l.kind == 1) {

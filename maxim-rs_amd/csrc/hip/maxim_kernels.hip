@@ -3,3 +3,4 @@
 #include "stream_ops.h"
 #include "gemm.h"
 #include "conv.h"
+#include "pointwise.h"

@@ -1,0 +1,267 @@
+// Streaming fp32 MFMA kernels for the Dense-shaped ops whose reduction is
+// short next to their streamed axis: every 1x1 conv (K = c_in <= 512 over
+// up to 286720 pixels) and both GateMm modes. Operands go straight from
+// memory into the matrix cores with 128-bit loads (no LDS staging): each wave
+// owns a 64 x (16 * TMW) output tile, or a quarter of its reduction, so a CU
+// keeps many independent waves in flight and the epilogue of one overlaps
+// the loads of another.
+//
+// Two layouts share one body (D = the 16x16 MFMA tile, lane l = 16g + i):
+//
+//   CH  Y[m][n] = bias[m] + sum_k W[m][k] X[k][n]       (conv1x1, GateMm mode 0)
+//       A operand = X^T: lane i of tile j supplies pixel n0 + 16 (i % 4) +
+//       4 (i / 4) + j, so one 128-bit load feeds four tiles (and the sixteen
+//       lanes of a row still read 256 contiguous bytes), and the output
+//       D_j[4g + r][i] = Y[m0 + i][n0 + 16r + 4g + j]: for each r the four
+//       lanes of a channel hold 16 adjacent pixels, one 64-byte run per store.
+//   RW  Y[n][a] = bias[a] + sum_k X[n][k] W[a][k]       (GateMm mode 1)
+//       A operand = W, B operand = X^T, so a lane holds four consecutive
+//       outputs of one row: D[4g + r][i] = Y[n0 + 16j + i][a0 + 4g + r].
+//
+// The reduction runs in supersteps of 16: within one, lane group g supplies
+// k = 16 S + 4 g + t at MFMA step t, which covers the 16 k's exactly once and
+// lets each lane fetch its four k's of a row with one 128-bit load.
+#pragma once
+
+#include "common.h"
+
+namespace pw {
+
+enum { CH = 0, RW = 1 };
+
+__device__ __forceinline__ float comp(const float4 &v, int t) {
+    return t == 0 ? v.x : t == 1 ? v.y : t == 2 ? v.z : v.w;
+}
+
+// GemmArgs as used here: A = W ([M][K] for CH, [N][K] for RW), B = X
+// ([K][N] for CH, [M][K] for RW), C = Y; M is the weight-output dimension for
+// CH and the row count for RW. Preconditions (checked by the host): K % 16 ==
+// 0 (K % 64 == 0 when KS = 4), N % 4 == 0, every pointer 16-byte aligned,
+// batch strides % 4 == 0.
+//
+// Work unit: one output tile of 64 streamed elements x TW weight outputs.
+// KS = 1: every wave owns a tile; KS = 4: the four waves of a block split one
+// tile's reduction into quarters and add the partial sums in LDS in a fixed
+// order (wave 0 + 1 + 2 + 3), for the shapes with too few tiles to fill the
+// chip.
+//
+// Operand loads are clamped into range instead of guarded: an X column or
+// weight row past the edge only feeds output rows/columns of the MFMA tile
+// that are never stored, so no branch or select sits between the loads and
+// the matrix cores. The reduction ping-pongs between two register buffers,
+// so the loads of superstep s + 1 are in flight while superstep s multiplies.
+template <int LAYOUT, int TMW, int KS, bool FUSED>
+__device__ void body(const GemmArgs &a) {
+    constexpr int TW = 16 * TMW;    // weight outputs per tile
+    constexpr int NACC = 16 * TMW;  // accumulator floats per lane
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int i = lane & 15, g = lane >> 4;
+    const int M = a.M, N = a.N, K = a.K;
+    const int wout = LAYOUT == CH ? M : N;
+    const int slen = LAYOUT == CH ? N : M;
+    const int nib = (wout + TW - 1) / TW;
+    const int ntiles = nib * ((slen + 63) / 64);  // < 2^31, checked by the host
+    const int b = blockIdx.y;
+    const float *W = a.A + (int64_t)b * a.sA;
+    const float *X = a.B + (int64_t)b * a.sB;
+    float *Y = a.C + (int64_t)b * a.sC;
+    const int64_t xstep = LAYOUT == CH ? 16 * (int64_t)N : 16;  // one superstep
+
+    // One XCD per contiguous range of blocks, so neighbouring tiles (which
+    // share operands) meet in the same L2.
+    int unit = blockIdx.x;
+    const int nb = gridDim.x;
+    if ((nb & 7) == 0) unit = (unit & 7) * (nb >> 3) + (unit >> 3);
+    const int tile = KS == 1 ? unit * 4 + wave : unit;
+    if (tile >= ntiles) return;  // KS = 4: the whole block
+    const int nS = K / 16;
+    const int S0 = KS == 1 ? 0 : wave * (nS / 4);
+    const int nSw = KS == 1 ? nS : nS / 4;  // supersteps of this wave
+
+    const int w0 = (tile % nib) * TW;
+    const int s0 = (tile / nib) * 64;
+    // This lane's operand streams at the wave's first superstep.
+    const float *wp[TMW];
+#pragma unroll
+    for (int mt = 0; mt < TMW; ++mt)
+        wp[mt] = W + (int64_t)min(w0 + mt * 16 + i, wout - 1) * K + 4 * g + S0 * 16;
+    const float *xp[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        if (LAYOUT == CH)  // row k = 16 S + 4 g + q, elements s0 + 16 (i % 4) + 4 (i / 4) .. + 3
+            xp[q] = X + (int64_t)(4 * g + q) * N + min(s0 + 16 * (i & 3) + 4 * (i >> 2), N - 4) + S0 * xstep;
+        else               // row s0 + 16 q + i, k = 16 S + 4 g .. + 3
+            xp[q] = X + (int64_t)min(s0 + 16 * q + i, M - 1) * K + 4 * g + S0 * xstep;
+    }
+
+    f32x4 acc[4][TMW];
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int mt = 0; mt < TMW; ++mt) acc[j][mt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+
+    auto load = [&](int s, float4 *xv, float4 *wv) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) xv[q] = ld4(xp[q] + s * xstep);
+#pragma unroll
+        for (int mt = 0; mt < TMW; ++mt) wv[mt] = ld4(wp[mt] + s * 16);
+    };
+    auto mma = [&](const float4 *xv, const float4 *wv) {
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+#pragma unroll
+                for (int mt = 0; mt < TMW; ++mt) {
+                    if (LAYOUT == CH)
+                        acc[j][mt] = mfma16(comp(xv[t], j), comp(wv[mt], t), acc[j][mt]);
+                    else
+                        acc[j][mt] = mfma16(comp(wv[mt], t), comp(xv[j], t), acc[j][mt]);
+                }
+    };
+    // The bias of this lane's outputs, fetched before the reduction.
+    float4 bias[TMW];
+#pragma unroll
+    for (int mt = 0; mt < TMW; ++mt) {
+        if (!a.bias) continue;
+        if (LAYOUT == CH) bias[mt].x = a.bias[min(w0 + mt * 16 + i, wout - 1)];
+        else bias[mt] = ld4(a.bias + min(w0 + mt * 16 + 4 * g, wout - 4));
+    }
+
+    float4 xa[4], wa[TMW], xb[4], wb[TMW];
+    load(0, xa, wa);
+    int s = 0;
+    for (; s + 2 <= nSw; s += 2) {
+        load(s + 1, xb, wb);
+        mma(xa, wa);
+        // unconditional (the last one re-reads the final superstep), so the
+        // wait before the next multiply counts only the loads it needs
+        load(min(s + 2, nSw - 1), xa, wa);
+        mma(xb, wb);
+    }
+    if (s < nSw) mma(xa, wa);
+
+    __shared__ float red[KS == 1 ? 1 : 4 * NACC * 64];
+    const int64_t cbase = (int64_t)b * a.sC;
+    if (KS == 4) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int mt = 0; mt < TMW; ++mt)
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+                    red[((wave * NACC) + (j * TMW + mt) * 4 + r) * 64 + lane] = acc[j][mt][r];
+        __syncthreads();
+    }
+    // Slot k of this lane: (mt, x) = (k / 4, k % 4) with KS = 1, and
+    // (k, wave) with KS = 4 (the wave's share of the slots).
+    constexpr int NK = KS == 1 ? 4 * TMW : TMW;
+    auto where = [&](int k, int64_t &off) -> bool {
+        const int mt = KS == 1 ? k / 4 : k, x = KS == 1 ? k % 4 : wave;
+        if (LAYOUT == CH) {
+            const int m = w0 + mt * 16 + i, n = s0 + 16 * x + 4 * g;
+            off = (int64_t)m * N + n;
+            return m < M && n < N;
+        }
+        const int row = s0 + 16 * x + i, c = w0 + mt * 16 + 4 * g;
+        off = (int64_t)row * N + c;
+        return row < M && c < N;
+    };
+    // The fused epilogue's operands are fetched one slot ahead, so their
+    // latency overlaps the previous slot's arithmetic and store (the
+    // compiler cannot move a load above a store that might alias it).
+    float4 ou[2], o1[2], o2[2];
+    auto operands = [&](int k, int buf) {
+        int64_t off;
+        const bool ok = where(k, off);
+        const int64_t at = cbase + (ok ? off : 0);
+        if (a.e.u) ou[buf] = ld4(a.e.u + at);
+        if (a.e.r1) o1[buf] = ld4(a.e.r1 + at);
+        if (a.e.r2) o2[buf] = ld4(a.e.r2 + at);
+    };
+    if (FUSED) operands(0, 0);
+#pragma unroll
+    for (int k = 0; k < NK; ++k) {
+        if (FUSED && k + 1 < NK) operands(k + 1, (k + 1) & 1);
+        const int mt = KS == 1 ? k / 4 : k, x = KS == 1 ? k % 4 : wave;
+        int64_t off;
+        if (!where(k, off)) continue;
+        float v[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            // CH: v[u] = Y[m][n + u] is acc[u][mt][x]; RW: v[u] = Y[row][c + u] is acc[x][mt][u]
+            const int j = LAYOUT == CH ? u : x, r = LAYOUT == CH ? x : u;
+            if (KS == 1) {
+                v[u] = acc[j][mt][r];
+            } else {
+                const int q = (j * TMW + mt) * 4 + r;
+                float t = red[q * 64 + lane];
+                t = t + red[(NACC + q) * 64 + lane];
+                t = t + red[(2 * NACC + q) * 64 + lane];
+                v[u] = t + red[(3 * NACC + q) * 64 + lane];
+            }
+        }
+        if (a.bias) {
+            if (LAYOUT == CH) {
+                const float bb = bias[mt].x;
+#pragma unroll
+                for (int u = 0; u < 4; ++u) v[u] = bb + v[u];
+            } else {
+                const float4 bb = bias[mt];
+                v[0] = bb.x + v[0];
+                v[1] = bb.y + v[1];
+                v[2] = bb.z + v[2];
+                v[3] = bb.w + v[3];
+            }
+        }
+        if (FUSED) {
+            const int bi = k & 1;
+            if (a.e.u) {
+                v[0] = ou[bi].x * (v[0] + 1.0f);
+                v[1] = ou[bi].y * (v[1] + 1.0f);
+                v[2] = ou[bi].z * (v[2] + 1.0f);
+                v[3] = ou[bi].w * (v[3] + 1.0f);
+            }
+            if (a.e.act == MXK_ACT_GELU) {
+#pragma unroll
+                for (int u = 0; u < 4; ++u) v[u] = gelu_erf(v[u]);
+            } else if (a.e.act == MXK_ACT_LRELU) {
+#pragma unroll
+                for (int u = 0; u < 4; ++u) v[u] = v[u] >= 0.0f ? v[u] : a.e.slope * v[u];
+            }
+            if (a.e.r1) {
+                v[0] = v[0] + o1[bi].x;
+                v[1] = v[1] + o1[bi].y;
+                v[2] = v[2] + o1[bi].z;
+                v[3] = v[3] + o1[bi].w;
+            }
+            if (a.e.r2) {
+                v[0] = v[0] + o2[bi].x;
+                v[1] = v[1] + o2[bi].y;
+                v[2] = v[2] + o2[bi].z;
+                v[3] = v[3] + o2[bi].w;
+            }
+        }
+        st4(Y + off, make_float4(v[0], v[1], v[2], v[3]));
+    }
+}
+
+}  // namespace pw
+
+// mx_pw_{ch,rw}<TMW>[_k4][_f]: 256 threads; _k4 splits the reduction over
+// the block's four waves.
+#define MXK_PW1(LNAME, LAYOUT, TMW, KS, SUF)                                                       \
+    extern "C" __global__ __launch_bounds__(256) void mx_pw_##LNAME##TMW##SUF(GemmArgs a) {        \
+        pw::body<pw::LAYOUT, TMW, KS, false>(a);                                                   \
+    }                                                                                               \
+    extern "C" __global__ __launch_bounds__(256) void mx_pw_##LNAME##TMW##SUF##_f(GemmArgs a) {    \
+        pw::body<pw::LAYOUT, TMW, KS, true>(a);                                                    \
+    }
+#define MXK_PW(LNAME, LAYOUT, TMW) MXK_PW1(LNAME, LAYOUT, TMW, 1, ) MXK_PW1(LNAME, LAYOUT, TMW, 4, _k4)
+MXK_PW(ch, CH, 1)
+MXK_PW(ch, CH, 2)
+MXK_PW(ch, CH, 4)
+MXK_PW(rw, RW, 1)
+MXK_PW(rw, RW, 2)
+MXK_PW(rw, RW, 4)

@@ -1,0 +1,154 @@
+"""Edge shapes of the streaming matrix-core kernels (mx_pw_*) against the CPU
+oracle, and of the executor's fallback to the tiled GEMM.
+
+The streaming kernels own 64-element tiles of the streamed axis and 16, 32
+or 64 weight outputs per wave, and split reductions of 128 and more over a
+block's four waves. These cases put every edge inside one op: streamed
+lengths that are not a multiple of 64, weight-output counts that leave a
+partial block, reductions with and without the split, GateMm in both modes,
+a plane that is not a multiple of four (the tiled GEMM takes the op), and
+fused epilogues whose extra operand is not 16-byte aligned (the executor
+swaps in the tiled kernel's fused form for that step).
+GEMM bar: max|d| <= 1e-4 * max|cpu| (matrix-core reduction order).
+"""
+
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+
+def he(rng, shape, fan_in):
+    return (rng.standard_normal(shape) * np.sqrt(2.0 / fan_in)).astype(np.float32)
+
+
+def check(got, want, label):
+    err = float(np.abs(got.astype(np.float64) - want).max())
+    scale = float(np.abs(want).max())
+    print("%s: max|cpu| %.3g, max-abs %.3g, relative %.3g" % (label, scale, err, err / scale), flush=True)
+    assert np.isfinite(got).all(), label
+    assert err <= 1e-4 * scale, label
+
+
+def run_plan(cp, inputs, out):
+    """Write every input buffer, run all ops through the fused program,
+    return the output buffer and the kernel of each step."""
+    from maxim_amd import hip as H
+    gpu = H.Gpu(cp)
+    for b, v in inputs.items():
+        gpu.write_buf(b, v)
+    gpu.run_ops(0, len(cp.ops))
+    got = gpu.read_buf(out).reshape(cp.bufs[out])
+    return got, gpu.steps()
+
+
+def oracle_plan(cp, inputs, out):
+    from oracle import oracle as O
+    arena = np.zeros(cp.arena_len, np.float32)
+    for b, v in inputs.items():
+        o = int(cp.offs[b])
+        arena[o:o + v.size] = v.ravel()
+    O.run(cp, arena)
+    o = int(cp.offs[out])
+    return arena[o:o + cp.buf_len(out)].reshape(cp.bufs[out])
+
+
+@pytest.mark.parametrize("ci,co,h,w", [
+    (16, 40, 12, 20),    # K 16, two weight blocks (the second partial), 240 pixels (ragged)
+    (48, 24, 8, 30),     # K 48, one partial 32-wide block
+    (192, 64, 10, 26),   # K 192: split reduction, 260 pixels
+    (256, 136, 6, 14),   # K 256: 64-wide blocks, the last one 8 wide
+    (32, 8, 16, 16),     # 16-wide blocks, half used
+    (24, 32, 7, 9),      # 63 pixels: not a multiple of four, tiled GEMM
+    (64, 32, 64, 64),    # the level-0 shape class
+])
+def test_conv1x1_edges(gpu_ok, ci, co, h, w):
+    from maxim_amd import plan as P
+    from oracle import oracle as O
+    rng = np.random.default_rng(ci * 1000 + co)
+    x = rng.standard_normal((ci, h, w)).astype(np.float32)
+    wt = he(rng, (co, ci), ci)
+    b = (rng.standard_normal(co) * 0.1).astype(np.float32)
+    op = P.make_op(P.CONV1X1, dst=1, src=0, w=0, bias=1, c_in=ci, c_out=co, h=h, wd=w)
+    cp = P.CustomPlan([(ci, h, w), (co, h, w)], [op], [wt, b], input=0, output=1)
+    got, steps = run_plan(cp, {0: x}, 1)
+    print("kernel", steps[0][2])
+    assert steps[0][2].startswith("mx_pw_" if (h * w) % 4 == 0 else "mx_gemm_")
+    check(got, O.conv1x1(x, wt, b), "conv1x1 %d->%d @%dx%d" % (ci, co, h, w))
+
+
+@pytest.mark.parametrize("c,outer,inner,mode", [
+    (3, 64, 20, 0),      # K 64, few tiles: split reduction; 20 columns (ragged)
+    (2, 48, 36, 0),      # K 48, 48 outputs (partial block)
+    (1, 256, 40, 0),     # K 256, 64-wide blocks
+    (3, 20, 64, 1),      # row layout, 60 rows (ragged), K 64
+    (2, 36, 48, 1),      # row layout, K 48, 48 columns
+    (1, 40, 256, 1),     # row layout, K 256
+    (2, 64, 70, 0),      # 70 columns: not a multiple of four, tiled GEMM
+])
+def test_gate_mm_edges(gpu_ok, c, outer, inner, mode):
+    from maxim_amd import plan as P
+    from oracle import oracle as O
+    rng = np.random.default_rng(c * 100 + outer + inner + mode)
+    k = outer if mode == 0 else inner
+    x = rng.standard_normal((c, outer, inner)).astype(np.float32)
+    wt = he(rng, (k, k), k)
+    b = (rng.standard_normal(k) * 0.1).astype(np.float32)
+    op = P.make_op(P.GATE_MM, dst=1, src=0, w=0, bias=1, c=c, mode=mode, p=[outer, inner])
+    cp = P.CustomPlan([(c, outer, inner), (c, outer, inner)], [op], [wt, b], input=0, output=1)
+    got, steps = run_plan(cp, {0: x}, 1)
+    print("kernel", steps[0][2])
+    check(got, O.gate_mm(x, wt, b, mode), "gate_mm c=%d %dx%d mode %d" % (c, outer, inner, mode))
+
+
+def fused_case(kind, misalign):
+    """conv1x1 feeding GELU or a residual add, or GateMm feeding the gate
+    multiply; with `misalign` the epilogue's extra operand (R) starts one
+    float past a 16-byte boundary. Buffers: X, pad, R, pad, T, Y."""
+    from maxim_amd import plan as P
+    rng = np.random.default_rng(7 + misalign)
+    if kind == "gate":
+        c, outer, inner = 8, 32, 40          # mode 0: K = 32 over 40 columns
+        xs = ys = (c, outer, inner)
+    else:
+        ci, co, h, w = 32, 64, 8, 40
+        xs, ys = (ci, h, w), (co, h, w)
+    bufs = [xs, (1, 1, 1 if misalign else 4), ys, (1, 1, 3 if misalign else 4), ys, ys]
+    X, R, T, Y = 0, 2, 4, 5
+    n = ys[0] * ys[1] * ys[2]
+    inputs = {X: rng.standard_normal(xs).astype(np.float32),
+              R: rng.standard_normal(ys).astype(np.float32)}
+    if kind == "gate":
+        wt = he(rng, (outer, outer), outer)
+        b = (rng.standard_normal(outer) * 0.1).astype(np.float32)
+        ops = [P.make_op(P.GATE_MM, dst=T, src=X, w=0, bias=1, c=c, mode=0, p=[outer, inner]),
+               P.make_op(P.GATE_APPLY, dst=Y, src=R, src2=T, n=n)]
+    else:
+        wt = he(rng, (co, ci), ci)
+        b = (rng.standard_normal(co) * 0.1).astype(np.float32)
+        conv = P.make_op(P.CONV1X1, dst=T, src=X, w=0, bias=1, c_in=ci, c_out=co, h=h, wd=w)
+        if kind == "gelu":
+            ops = [conv, P.make_op(P.GELU, dst=Y, src=T, n=n)]
+        else:
+            ops = [conv, P.make_op(P.ADD, dst=Y, src=T, src2=R, n=n)]
+    cp = P.CustomPlan(bufs, ops, [wt, b], input=X, output=Y, align=1)
+    return cp, inputs, Y
+
+
+@pytest.mark.parametrize("kind", ["gelu", "add", "gate"])
+@pytest.mark.parametrize("misalign", [0, 1])
+def test_fused_epilogue_alignment(gpu_ok, kind, misalign):
+    cp, inputs, Y = fused_case(kind, misalign)
+    r_off = int(cp.offs[2])
+    assert (r_off % 4 != 0) == bool(misalign) and int(cp.offs[4]) % 4 == 0
+    got, steps = run_plan(cp, inputs, Y)
+    print("steps", steps)
+    assert len(steps) == 1, "the pair did not fuse"
+    kern = steps[0][2]
+    assert kern.endswith("_f")
+    if misalign and kind != "gelu":
+        assert kern.startswith("mx_gemm_"), kern   # 128-bit epilogue loads need alignment
+    else:
+        assert kern.startswith("mx_pw_"), kern
+    want = oracle_plan(cp, inputs, Y)
+    check(got, want, "fused %s, operand misaligned %d" % (kind, misalign))
