@@ -595,10 +595,9 @@ Gpu::Gpu(const mx_plan_desc *p) : H(hip()), doff(pg.doff) {
                 break;
             }
             case MX_OP_GATE_MM: {
-                if (o.mode == 0) {
-                    as_is(o.w);
-                } else {
-                    // [a][t] -> [t][a], the B operand of X . W^T
+                as_is(o.w);  // [a][t]: the streaming kernels' layout, both modes
+                if (o.mode == 1) {
+                    // [a][t] -> [t][a], the B operand of the tiled X . W^T
                     const int64_t k = o.p[1];
                     const float *w = p->weights[o.w];
                     std::vector<float> t((size_t)(k * k));
@@ -662,7 +661,9 @@ void Gpu::build_launches(const mx_plan_desc *p, const std::vector<int64_t> &woff
                          const std::vector<std::array<int, 2>> &maxt) {
     auto B = [&](int64_t id) { return arena + doff[id]; };
     auto W = [&](int64_t id) -> const float * {
-        return id >= 0 ? reinterpret_cast<const float *>(wdev) + woff[id] : nullptr;
+        if (id < 0) return nullptr;
+        if (woff[id] < 0) throw Error("internal: weight " + std::to_string(id) + " was not uploaded");
+        return reinterpret_cast<const float *>(wdev) + woff[id];
     };
     auto X = [&](uint64_t i, int k) { return reinterpret_cast<const float *>(wdev) + extra[i][k]; };
     ops.assign(p->n_ops, {});

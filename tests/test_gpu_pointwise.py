@@ -98,6 +98,7 @@ def test_gate_mm_edges(gpu_ok, c, outer, inner, mode):
     cp = P.CustomPlan([(c, outer, inner), (c, outer, inner)], [op], [wt, b], input=0, output=1)
     got, steps = run_plan(cp, {0: x}, 1)
     print("kernel", steps[0][2])
+    assert steps[0][2].startswith("mx_pw_" if inner % 4 == 0 else "mx_gemm_")
     check(got, O.gate_mm(x, wt, b, mode), "gate_mm c=%d %dx%d mode %d" % (c, outer, inner, mode))
 
 
