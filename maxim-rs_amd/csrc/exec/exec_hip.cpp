@@ -39,7 +39,7 @@ struct Launch {
     const char *name = "";
     unsigned g[3] = {1, 1, 1};
     unsigned b[3] = {MXK_BLOCK, 1, 1};
-    alignas(16) unsigned char a0[128];
+    alignas(16) unsigned char a0[192];
     alignas(16) unsigned char a1[32];
     int nparams = 1;
     int kind = 0;  // 1: a0 holds GemmArgs (plain epilogue), 2: ConvArgs
@@ -50,6 +50,7 @@ struct Launch {
 struct Step {
     uint64_t first, last;
     std::vector<Launch> launches;
+    size_t main = 0;  // the launch that names the step in reports
 };
 
 template <typename T>
@@ -203,6 +204,7 @@ std::string conv_name(ConvCfg c, bool k3) {
 // ops fuse into which steps, and where every buffer lives in the device arena.
 struct StepSpec {
     uint64_t first = 0, last = 0;
+    int64_t ln = -1;  // a LayerNorm op folded into the next op's GEMM (== first)
     int64_t out = -1, u = -1, r1 = -1, r2 = -1;
     int act = MXK_ACT_NONE;
     float slope = 0.0f;
@@ -231,7 +233,7 @@ public:
     unsigned char *wdev = nullptr;
     uint64_t wbytes = 0;
     float *scratch = nullptr;
-    uint64_t scratch_len = 0;
+    uint64_t scratch_len = 0, ln_off = 0;
     uint64_t n_ops = 0, n_bufs = 0;
     std::vector<std::vector<Launch>> ops;
     uint64_t launched = 0, kernels = 0;
@@ -630,7 +632,13 @@ Gpu::Gpu(const mx_plan_desc *p) : H(hip()), doff(pg.doff) {
 
     // Size the pass before allocating it, and refuse with the numbers.
     wbytes = blob.size() * 4;
-    scratch_len = std::max<uint64_t>(mean_scratch, 64);
+    // Scratch: channel-mean partial sums, then the statistics of a folded
+    // LayerNorm ([2][hw], one step at a time).
+    ln_off = (mean_scratch + 63) & ~(uint64_t)63;
+    uint64_t ln_need = 0;
+    for (const StepSpec &sp : pg.specs)
+        if (sp.ln >= 0) ln_need = std::max<uint64_t>(ln_need, 2 * (uint64_t)p->ops[sp.ln].hw);
+    scratch_len = std::max<uint64_t>(ln_off + ln_need, 64);
     const uint64_t need = arena_len * 4 + wbytes + scratch_len * 4;
     size_t free_b = 0, total_b = 0;
     if (H.hipMemGetInfo(&free_b, &total_b) == 0 && need > free_b) {
@@ -1033,6 +1041,60 @@ void Program::plan_fusion(const mx_plan_desc *p, bool require_clear) {
         return true;
     };
 
+    // Extend `sp` with the reader of producer g's output, when a rule applies.
+    auto epilogue = [&](uint64_t g, StepSpec &sp) {
+        const mx_op &o = p->ops[g];
+        if (!(g + 1 < p->n_ops && (gemm_op(o) || o.kind == MX_OP_CONV3X3) && only_reader(o.dst, g, g + 1))) return;
+        const int64_t x = o.dst;
+        const mx_op &n1 = p->ops[g + 1];
+        std::vector<int64_t> reads = reads_of(o);
+        if (sp.ln >= 0) reads.push_back(p->ops[sp.ln].src);
+        StepSpec f = sp;
+        if (o.kind == MX_OP_GATE_MM && n1.kind == MX_OP_GATE_APPLY && n1.src2 == x && n1.src != x &&
+            whole(n1, x)) {
+            f.u = n1.src;
+            f.out = n1.dst;
+            f.last = g + 2;
+        } else if (o.kind == MX_OP_CONV1X1 && n1.kind == MX_OP_GELU && n1.src == x && whole(n1, x)) {
+            f.act = MXK_ACT_GELU;
+            f.out = n1.dst;
+            f.last = g + 2;
+        } else if (o.kind == MX_OP_CONV3X3 && n1.kind == MX_OP_LRELU && n1.src == x && whole(n1, x)) {
+            f.act = MXK_ACT_LRELU;
+            f.slope = n1.slope;
+            f.out = n1.dst;
+            f.last = g + 2;
+        } else if (o.kind == MX_OP_CONV1X1 && n1.kind == MX_OP_COPY && n1.src == x && whole(n1, x)) {
+            f.out = n1.dst;
+            f.last = g + 2;
+        } else if (o.kind == MX_OP_CONV1X1 && n1.kind == MX_OP_ADD && (n1.src == x) != (n1.src2 == x) &&
+                   whole(n1, x)) {
+            f.r1 = n1.src == x ? n1.src2 : n1.src;
+            f.out = n1.dst;
+            f.last = g + 2;
+            if (g + 2 < p->n_ops) {
+                const mx_op &n2 = p->ops[g + 2];
+                const int64_t y = f.out;
+                if (n2.kind == MX_OP_ADD && (n2.src == y) != (n2.src2 == y) && whole(n2, y) &&
+                    only_reader(y, g + 1, g + 2)) {
+                    const int64_t r2 = n2.src == y ? n2.src2 : n2.src;
+                    std::vector<int64_t> rr = reads;
+                    rr.insert(rr.end(), {f.r1, r2, y});
+                    if (clear_of(n2.dst, rr)) {
+                        f.r2 = r2;
+                        f.out = n2.dst;
+                        f.last = g + 3;
+                    }
+                }
+            }
+        }
+        if (f.out >= 0) {
+            for (int64_t r : {f.u, f.r1, f.r2})
+                if (r >= 0) reads.push_back(r);
+            if (clear_of(f.out, reads)) sp = f;
+        }
+    };
+
     specs.clear();
     fused_ops = 0;
     for (uint64_t i = 0; i < p->n_ops;) {
@@ -1040,53 +1102,19 @@ void Program::plan_fusion(const mx_plan_desc *p, bool require_clear) {
         StepSpec sp;
         sp.first = i;
         sp.last = i + 1;
-        if (i + 1 < p->n_ops && (gemm_op(o) || o.kind == MX_OP_CONV3X3) && only_reader(o.dst, i, i + 1)) {
-            const int64_t x = o.dst;
+        // LayerNorm -> 1x1 conv: the conv's GEMM reads the LayerNorm's input
+        // and normalises it on the way in (the streaming kernels' _ln form).
+        if (o.kind == MX_OP_CHAN_LN && i + 1 < p->n_ops) {
             const mx_op &n1 = p->ops[i + 1];
-            std::vector<int64_t> reads = reads_of(o);
-            StepSpec f = sp;
-            if (o.kind == MX_OP_GATE_MM && n1.kind == MX_OP_GATE_APPLY && n1.src2 == x && n1.src != x &&
-                whole(n1, x)) {
-                f.u = n1.src;
-                f.out = n1.dst;
-                f.last = i + 2;
-            } else if (o.kind == MX_OP_CONV1X1 && n1.kind == MX_OP_GELU && n1.src == x && whole(n1, x)) {
-                f.act = MXK_ACT_GELU;
-                f.out = n1.dst;
-                f.last = i + 2;
-            } else if (o.kind == MX_OP_CONV3X3 && n1.kind == MX_OP_LRELU && n1.src == x && whole(n1, x)) {
-                f.act = MXK_ACT_LRELU;
-                f.slope = n1.slope;
-                f.out = n1.dst;
-                f.last = i + 2;
-            } else if (o.kind == MX_OP_CONV1X1 && n1.kind == MX_OP_COPY && n1.src == x && whole(n1, x)) {
-                f.out = n1.dst;
-                f.last = i + 2;
-            } else if (o.kind == MX_OP_CONV1X1 && n1.kind == MX_OP_ADD && (n1.src == x) != (n1.src2 == x) &&
-                       whole(n1, x)) {
-                f.r1 = n1.src == x ? n1.src2 : n1.src;
-                f.out = n1.dst;
-                f.last = i + 2;
-                if (i + 2 < p->n_ops) {
-                    const mx_op &n2 = p->ops[i + 2];
-                    const int64_t y = f.out;
-                    if (n2.kind == MX_OP_ADD && (n2.src == y) != (n2.src2 == y) && whole(n2, y) &&
-                        only_reader(y, i + 1, i + 2)) {
-                        const int64_t r2 = n2.src == y ? n2.src2 : n2.src;
-                        if (clear_of(n2.dst, {f.r1, r2, y})) {
-                            f.r2 = r2;
-                            f.out = n2.dst;
-                            f.last = i + 3;
-                        }
-                    }
-                }
-            }
-            if (f.out >= 0) {
-                for (int64_t r : {f.u, f.r1, f.r2})
-                    if (r >= 0) reads.push_back(r);
-                if (clear_of(f.out, reads)) sp = f;
+            if (n1.kind == MX_OP_CONV1X1 && n1.src == o.dst && n1.h * n1.wd == o.hw && o.hw > 1 &&
+                n1.c_in == o.c && o.hw % 4 == 0 && o.c % 16 == 0 && only_reader(o.dst, i, i + 1) &&
+                clear_of(n1.dst, {o.src})) {
+                sp.ln = (int64_t)i;
+                sp.last = i + 2;
+                epilogue(i + 1, sp);
             }
         }
+        if (sp.ln < 0) epilogue(i, sp);
         fused_ops += sp.last - sp.first - 1;
         specs.push_back(sp);
         i = sp.last;
@@ -1176,12 +1204,8 @@ void Program::layout(const mx_plan_desc *p, bool repack) {
 // step is the producer's launch with its destination and epilogue patched.
 void Gpu::build_program(const mx_plan_desc *p) {
     auto dev = [&](int64_t id) -> float * { return id >= 0 ? arena + doff[id] : nullptr; };
-    prog.clear();
-    for (const StepSpec &sp : pg.specs) {
-        if (sp.out < 0) {
-            prog.push_back(Step{sp.first, sp.last, ops[sp.first]});
-            continue;
-        }
+    // The producer g's launch with the step's epilogue applied (kernel + _f).
+    auto with_epilogue = [&](const StepSpec &sp, uint64_t g, const Launch &base) {
         Epilogue e{};
         e.u = dev(sp.u);
         e.r1 = dev(sp.r1);
@@ -1191,9 +1215,9 @@ void Gpu::build_program(const mx_plan_desc *p) {
         // 128-bit stores need every array the epilogue indexes like the
         // output on a 16-byte boundary.
         const bool ealign = aligned(e.u, 16) && aligned(e.r1, 16) && aligned(e.r2, 16);
-        Launch l = ops[sp.first][0];
+        Launch l = base;
         if (!strncmp(l.name, "mx_pw_", 6) && !(ealign && aligned(dev(sp.out), 16)))
-            l = alt[sp.first][0];  // the streaming kernels store 128 bits at a time
+            l = alt[g][0];  // the streaming kernels store 128 bits at a time
         l.name = intern(std::string(l.name) + "_f");
         l.f = fn(l.name);
         if (l.kind == 1) {
@@ -1213,9 +1237,59 @@ void Gpu::build_program(const mx_plan_desc *p) {
         } else {
             throw Error("internal: a fused step whose producer has no epilogue");
         }
-        prog.push_back(Step{sp.first, sp.last, {l}});
+        return l;
+    };
+    prog.clear();
+    for (const StepSpec &sp : pg.specs) {
+        if (sp.ln < 0) {
+            if (sp.out < 0) prog.push_back(Step{sp.first, sp.last, ops[sp.first]});
+            else prog.push_back(Step{sp.first, sp.last, {with_epilogue(sp, sp.first, ops[sp.first][0])}});
+            continue;
+        }
+        // A LayerNorm folded into the next op's streaming GEMM: the
+        // statistics pass, then the GEMM reading the LayerNorm's input.
+        const uint64_t g = sp.first + 1;
+        const mx_op &ln = p->ops[sp.first];
+        const Launch &conv = ops[g][0];
+        ChanLnArgs la;
+        memcpy(&la, ops[sp.first][0].a0, sizeof la);
+        float *stats = scratch + ln_off;
+        const bool ok = !strncmp(conv.name, "mx_pw_ch", 8) && aligned(la.x, 16) && la.hw % 4 == 0;
+        Launch gl = sp.out < 0 ? conv : with_epilogue(sp, g, conv);
+        if (!ok || strncmp(gl.name, "mx_pw_ch", 8)) {
+            // not streaming (shape or alignment): the LayerNorm runs on its own
+            Step st{sp.first, sp.last, ops[sp.first]};
+            st.launches.push_back(gl);
+            st.main = st.launches.size() - 1;
+            prog.push_back(st);
+            continue;
+        }
+        ChanLnArgs sa = la;
+        sa.y = stats;
+        Launch sl;
+        if (ln.c == 64 || ln.c == 128) {
+            // the LayerNorm kernels' LDS tile, C x (8192 / C) pixels per block
+            // (measured faster than the register loop from 64 channels up)
+            sl = mk(ln.c == 64 ? "mx_chan_ln_stats_c64" : "mx_chan_ln_stats_c128");
+            sl.g[0] = cdiv(ln.hw, 8192 / ln.c);
+        } else {
+            sl = mk("mx_chan_ln_stats");
+            sl.g[0] = cdiv((ln.hw + 3) / 4, MXK_BLOCK);
+        }
+        set_args(sl, sa);
+        const std::string gname = gl.name;
+        const bool f = gname.size() > 2 && gname.compare(gname.size() - 2, 2, "_f") == 0;
+        gl.name = intern((f ? gname.substr(0, gname.size() - 2) : gname) + "_ln" + (f ? "_f" : ""));
+        gl.f = fn(gl.name);
+        GemmArgs a;
+        memcpy(&a, gl.a0, sizeof a);
+        a.B = la.x;
+        a.ln = LnIn{stats, stats + ln.hw, la.scale, la.bias};
+        set_args(gl, a);
+        Step st{sp.first, sp.last, {sl, gl}};
+        st.main = 1;
+        prog.push_back(st);
     }
-    (void)p;
 }
 
 Gpu::~Gpu() {
@@ -1377,7 +1451,7 @@ int mxh_step_info(mxh_gpu *g, uint64_t i, uint64_t *first, uint64_t *last, const
         if (x.fusion) {
             a = x.prog[i].first;
             b = x.prog[i].last;
-            if (!x.prog[i].launches.empty()) k = x.prog[i].launches[0].name;
+            if (!x.prog[i].launches.empty()) k = x.prog[i].launches[x.prog[i].main].name;
         } else if (!x.ops[i].empty()) {
             k = x.ops[i][0].name;
         }

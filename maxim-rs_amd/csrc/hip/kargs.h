@@ -97,6 +97,13 @@ struct Epilogue {
     float slope;
 };
 
+// A channel LayerNorm folded into a GEMM's X operand (channel-major layout):
+// X[k][n] is used as (X[k][n] - mean[n]) * rstd[n] * scale[k] + bias[k], the
+// LayerNorm kernels' own expression, with mean/rstd from mx_chan_ln_stats.
+struct LnIn {
+    const float *mean, *rstd, *scale, *bias;
+};
+
 struct GemmArgs {
     const float *A;
     const float *B;
@@ -108,6 +115,7 @@ struct GemmArgs {
     int32_t co, wd;       // convT: output channels and input width
     int32_t cvec, pad;    // 1: C, u, r1, r2 are 16-byte aligned (128-bit stores)
     Epilogue e;
+    LnIn ln;
 };
 
 // Small GEMV for the plane-1 CALayer convs: y[o] = b[o] + sum_i w[o][i] x[i].

@@ -50,7 +50,7 @@ __device__ __forceinline__ float comp(const float4 &v, int t) {
 // that are never stored, so no branch or select sits between the loads and
 // the matrix cores. The reduction ping-pongs between two register buffers,
 // so the loads of superstep s + 1 are in flight while superstep s multiplies.
-template <int LAYOUT, int TMW, int KS, bool FUSED>
+template <int LAYOUT, int TMW, int KS, bool FUSED, bool LN>
 __device__ void body(const GemmArgs &a) {
     constexpr int TW = 16 * TMW;    // weight outputs per tile
     constexpr int NACC = 16 * TMW;  // accumulator floats per lane
@@ -101,13 +101,39 @@ __device__ void body(const GemmArgs &a) {
 #pragma unroll
         for (int mt = 0; mt < TMW; ++mt) acc[j][mt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 
-    auto load = [&](int s, float4 *xv, float4 *wv) {
+    // A folded LayerNorm (CH only): this lane's four pixels' statistics for
+    // the whole tile, and each superstep's scale/bias for k = 16 S + 4 g + q.
+    float4 lmean, lrstd;
+    const float *lsc = nullptr, *lbi = nullptr;
+    if (LN) {  // a single 1x1 conv (no batch): pixel n's statistics at n
+        const int n = min(s0 + 16 * (i & 3) + 4 * (i >> 2), N - 4);
+        lmean = ld4(a.ln.mean + n);
+        lrstd = ld4(a.ln.rstd + n);
+        lsc = a.ln.scale + 4 * g + S0 * 16;
+        lbi = a.ln.bias + 4 * g + S0 * 16;
+    }
+    auto load = [&](int s, float4 *xv, float4 *wv, float4 *lv) {
 #pragma unroll
         for (int q = 0; q < 4; ++q) xv[q] = ld4(xp[q] + s * xstep);
 #pragma unroll
         for (int mt = 0; mt < TMW; ++mt) wv[mt] = ld4(wp[mt] + s * 16);
+        if (LN) {
+            lv[0] = ld4(lsc + s * 16);
+            lv[1] = ld4(lbi + s * 16);
+        }
     };
-    auto mma = [&](const float4 *xv, const float4 *wv) {
+    auto norm = [&](float4 *xv, const float4 *lv) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const float w = comp(lv[0], q), c = comp(lv[1], q);
+            xv[q].x = (xv[q].x - lmean.x) * lrstd.x * w + c;
+            xv[q].y = (xv[q].y - lmean.y) * lrstd.y * w + c;
+            xv[q].z = (xv[q].z - lmean.z) * lrstd.z * w + c;
+            xv[q].w = (xv[q].w - lmean.w) * lrstd.w * w + c;
+        }
+    };
+    auto mma = [&](float4 *xv, const float4 *wv, const float4 *lv) {
+        if (LN) norm(xv, lv);
 #pragma unroll
         for (int t = 0; t < 4; ++t)
 #pragma unroll
@@ -129,18 +155,18 @@ __device__ void body(const GemmArgs &a) {
         else bias[mt] = ld4(a.bias + min(w0 + mt * 16 + 4 * g, wout - 4));
     }
 
-    float4 xa[4], wa[TMW], xb[4], wb[TMW];
-    load(0, xa, wa);
+    float4 xa[4], wa[TMW], la[2], xb[4], wb[TMW], lb[2];
+    load(0, xa, wa, la);
     int s = 0;
     for (; s + 2 <= nSw; s += 2) {
-        load(s + 1, xb, wb);
-        mma(xa, wa);
+        load(s + 1, xb, wb, lb);
+        mma(xa, wa, la);
         // unconditional (the last one re-reads the final superstep), so the
         // wait before the next multiply counts only the loads it needs
-        load(min(s + 2, nSw - 1), xa, wa);
-        mma(xb, wb);
+        load(min(s + 2, nSw - 1), xa, wa, la);
+        mma(xb, wb, lb);
     }
-    if (s < nSw) mma(xa, wa);
+    if (s < nSw) mma(xa, wa, la);
 
     __shared__ float red[KS == 1 ? 1 : 4 * NACC * 64];
     const int64_t cbase = (int64_t)b * a.sC;
@@ -249,19 +275,25 @@ __device__ void body(const GemmArgs &a) {
 
 }  // namespace pw
 
-// mx_pw_{ch,rw}<TMW>[_k4][_f]: 256 threads; _k4 splits the reduction over
-// the block's four waves.
-#define MXK_PW1(LNAME, LAYOUT, TMW, KS, SUF)                                                       \
+// mx_pw_{ch,rw}<TMW>[_k4][_ln][_f]: 256 threads; _k4 splits the reduction
+// over the block's four waves, _ln folds a channel LayerNorm into X (CH only),
+// _f applies the fused epilogue.
+#define MXK_PW1(LNAME, LAYOUT, TMW, KS, LN, SUF)                                                   \
     extern "C" __global__ __launch_bounds__(256) void mx_pw_##LNAME##TMW##SUF(GemmArgs a) {        \
-        pw::body<pw::LAYOUT, TMW, KS, false>(a);                                                   \
+        pw::body<pw::LAYOUT, TMW, KS, false, LN>(a);                                               \
     }                                                                                               \
     extern "C" __global__ __launch_bounds__(256) void mx_pw_##LNAME##TMW##SUF##_f(GemmArgs a) {    \
-        pw::body<pw::LAYOUT, TMW, KS, true>(a);                                                    \
+        pw::body<pw::LAYOUT, TMW, KS, true, LN>(a);                                                \
     }
-#define MXK_PW(LNAME, LAYOUT, TMW) MXK_PW1(LNAME, LAYOUT, TMW, 1, ) MXK_PW1(LNAME, LAYOUT, TMW, 4, _k4)
+#define MXK_PW(LNAME, LAYOUT, TMW) \
+    MXK_PW1(LNAME, LAYOUT, TMW, 1, false, ) MXK_PW1(LNAME, LAYOUT, TMW, 4, false, _k4)
+#define MXK_PW_LN(TMW) MXK_PW1(ch, CH, TMW, 1, true, _ln) MXK_PW1(ch, CH, TMW, 4, true, _k4_ln)
 MXK_PW(ch, CH, 1)
 MXK_PW(ch, CH, 2)
 MXK_PW(ch, CH, 4)
 MXK_PW(rw, RW, 1)
 MXK_PW(rw, RW, 2)
 MXK_PW(rw, RW, 4)
+MXK_PW_LN(1)
+MXK_PW_LN(2)
+MXK_PW_LN(4)

@@ -110,7 +110,9 @@ extern "C" __global__ __launch_bounds__(MXK_BLOCK) void mx_chan_scale_s(ChanScal
 // normalise and store. The staging is what keeps many loads in flight; the
 // serial part runs at LDS latency, not memory latency.
 
-template <int C, int P>
+// STATS: write only the statistics (mean into y[0 .. hw), 1 / std into
+// y[hw .. 2 hw)), for a LayerNorm folded into the next op's GEMM.
+template <int C, int P, bool STATS = false>
 __device__ void chan_ln_tile(const ChanLnArgs &a) {
     static_assert(C * P == 8192, "a 32 KiB tile");
     __shared__ float t[C][P];
@@ -145,9 +147,18 @@ __device__ void chan_ln_tile(const ChanLnArgs &a) {
         const float nf = (float)C;
         const float m = s1 / nf;
         const float var = s2 / nf - m * m;
+        const float r = 1.0f / sqrtf(fmaxf(var, 0.0f) + a.eps);
+        if (STATS) {
+            if (p0 + tid < a.hw) {
+                a.y[p0 + tid] = m;
+                a.y[a.hw + p0 + tid] = r;
+            }
+            return;
+        }
         st[0][tid] = m;
-        st[1][tid] = 1.0f / sqrtf(fmaxf(var, 0.0f) + a.eps);
+        st[1][tid] = r;
     }
+    if (STATS) return;
     __syncthreads();
     for (int i = tid; i < C * Q; i += MXK_BLOCK) {
         const int c = i / Q, q = (i % Q) * 4;
@@ -192,6 +203,50 @@ extern "C" __global__ __launch_bounds__(MXK_BLOCK) void mx_chan_ln_any(ChanLnArg
         int64_t i = (int64_t)c * a.hw + p;
         a.y[i] = (a.x[i] - m) * r * a.scale[c] + a.bias[c];
     }
+}
+
+// The per-pixel statistics alone, for a LayerNorm folded into the following
+// 1x1 conv: chan_ln_tile's staging, sums, order and expressions, so the
+// normalised values the GEMM forms from them are that kernel's to the bit.
+extern "C" __global__ __launch_bounds__(MXK_BLOCK) void mx_chan_ln_stats_c32(ChanLnArgs a) {
+    chan_ln_tile<32, 256, true>(a);
+}
+extern "C" __global__ __launch_bounds__(MXK_BLOCK) void mx_chan_ln_stats_c64(ChanLnArgs a) {
+    chan_ln_tile<64, 128, true>(a);
+}
+extern "C" __global__ __launch_bounds__(MXK_BLOCK) void mx_chan_ln_stats_c128(ChanLnArgs a) {
+    chan_ln_tile<128, 64, true>(a);
+}
+
+// Any channel count: four pixels per thread, the channel loop in registers.
+// Needs hw % 4 == 0 and 16-byte aligned x and y.
+extern "C" __global__ __launch_bounds__(MXK_BLOCK) void mx_chan_ln_stats(ChanLnArgs a) {
+    const int64_t p = ((int64_t)blockIdx.x * MXK_BLOCK + threadIdx.x) * 4;
+    if (p >= a.hw) return;
+    float s1[4] = {0.0f, 0.0f, 0.0f, 0.0f}, s2[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    const float *x = a.x + p;
+#pragma unroll 4
+    for (int c = 0; c < a.c; ++c) {
+        const float4 v = ld4(x + (int64_t)c * a.hw);
+        s1[0] += v.x;
+        s2[0] += v.x * v.x;
+        s1[1] += v.y;
+        s2[1] += v.y * v.y;
+        s1[2] += v.z;
+        s2[2] += v.z * v.z;
+        s1[3] += v.w;
+        s2[3] += v.w * v.w;
+    }
+    const float nf = (float)a.c;
+    float m[4], r[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+        m[u] = s1[u] / nf;
+        const float var = s2[u] / nf - m[u] * m[u];
+        r[u] = 1.0f / sqrtf(fmaxf(var, 0.0f) + a.eps);
+    }
+    st4(a.y + p, make_float4(m[0], m[1], m[2], m[3]));
+    st4(a.y + a.hw + p, make_float4(r[0], r[1], r[2], r[3]));
 }
 
 // ----------------------------------------------------------- channel mean

@@ -153,3 +153,38 @@ def test_fused_epilogue_alignment(gpu_ok, kind, misalign):
         assert kern.startswith("mx_pw_"), kern
     want = oracle_plan(cp, inputs, Y)
     check(got, want, "fused %s, operand misaligned %d" % (kind, misalign))
+
+
+@pytest.mark.parametrize("c,co,h,w,act", [
+    (32, 64, 8, 30, True),     # 240 pixels (ragged), GELU epilogue too
+    (48, 24, 6, 10, False),    # K 48
+    (128, 256, 8, 16, True),   # K 128: split reduction
+    (32, 32, 5, 7, False),     # 35 pixels: not folded, the LayerNorm runs on its own
+])
+def test_layernorm_folded_into_the_dense(gpu_ok, c, co, h, w, act):
+    """ChanLn -> Conv1x1 [-> Gelu] as one step: a statistics pass, then the
+    streaming GEMM normalising its operand on the way in. Compared with the
+    CPU path; the whole-model tests check it is bitwise the unfused pass."""
+    from maxim_amd import plan as P
+    rng = np.random.default_rng(c + co + h)
+    hw = h * w
+    x = (rng.standard_normal((c, h, w)) * 2.0 + 0.5).astype(np.float32)
+    scale = (1.0 + 0.1 * rng.standard_normal(c)).astype(np.float32)
+    bias = (0.1 * rng.standard_normal(c)).astype(np.float32)
+    wt = he(rng, (co, c), c)
+    b = (rng.standard_normal(co) * 0.1).astype(np.float32)
+    ops = [P.make_op(P.CHAN_LN, dst=1, src=0, scale=0, bias=1, c=c, hw=hw),
+           P.make_op(P.CONV1X1, dst=2, src=1, w=2, bias=3, c_in=c, c_out=co, h=h, wd=w)]
+    bufs = [(c, h, w), (c, h, w), (co, h, w)]
+    if act:
+        ops.append(P.make_op(P.GELU, dst=3, src=2, n=co * hw))
+        bufs.append((co, h, w))
+    out = len(bufs) - 1
+    cp = P.CustomPlan(bufs, ops, [scale, bias, wt, b], input=0, output=out)
+    got, steps = run_plan(cp, {0: x}, out)
+    print("steps", steps)
+    if hw % 4 == 0:
+        assert len(steps) == 1 and "_ln" in steps[0][2], steps
+    else:
+        assert [(a, b) for a, b, _ in steps] == [(0, 1), (1, 2)], steps
+    check(got, oracle_plan(cp, {0: x}, out), "ln %d -> conv1x1 %d->%d @%dx%d%s" % (c, c, co, h, w, " + gelu" if act else ""))
