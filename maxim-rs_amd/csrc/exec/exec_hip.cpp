@@ -202,8 +202,11 @@ std::string conv_name(ConvCfg c, bool k3) {
 
 // What the executor decides about a plan before touching the device: which
 // ops fuse into which steps, and where every buffer lives in the device arena.
+enum { RULE_NONE = 0, RULE_CA_MLP = 1, RULE_SCALE_ADD = 2 };
+
 struct StepSpec {
     uint64_t first = 0, last = 0;
+    int rule = RULE_NONE;  // a fusion that is not a producer's epilogue
     int64_t ln = -1;  // a LayerNorm op folded into the next op's GEMM (== first)
     int64_t out = -1, u = -1, r1 = -1, r2 = -1;
     int act = MXK_ACT_NONE;
@@ -717,7 +720,7 @@ void Gpu::build_launches(const mx_plan_desc *p, const std::vector<int64_t> &woff
                 break;
             }
             case MX_OP_CHAN_SCALE: {
-                ChanScaleArgs a{B(o.src), B(o.src2), B(o.dst), o.hw, o.c};
+                ChanScaleArgs a{B(o.src), B(o.src2), B(o.dst), o.hw, o.c, nullptr};
                 bool vec = o.hw % 4 == 0 && aligned(a.x, 16) && aligned(a.y, 16);
                 Launch l = mk(vec ? "mx_chan_scale_v4" : "mx_chan_scale_s");
                 l.g[0] = vec ? cdiv(o.hw / 4, MXK_BLOCK * 4) : cdiv(o.hw, MXK_BLOCK);
@@ -1102,9 +1105,37 @@ void Program::plan_fusion(const mx_plan_desc *p, bool require_clear) {
         StepSpec sp;
         sp.first = i;
         sp.last = i + 1;
+        // The CALayer's MLP: plane-1 Conv1x1 -> Lrelu -> plane-1 Conv1x1 ->
+        // Sigmoid, one block (mx_ca_mlp).
+        if (o.kind == MX_OP_CONV1X1 && o.h * o.wd == 1 && i + 3 < p->n_ops && o.c_out <= 1024) {
+            const mx_op &n1 = p->ops[i + 1], &n2 = p->ops[i + 2], &n3 = p->ops[i + 3];
+            if (n1.kind == MX_OP_LRELU && n1.src == o.dst && n1.n == o.c_out && n2.kind == MX_OP_CONV1X1 &&
+                n2.h * n2.wd == 1 && n2.src == n1.dst && n2.c_in == o.c_out && n2.c_out == o.c_in &&
+                n3.kind == MX_OP_SIGMOID && n3.src == n2.dst && n3.n == n2.c_out && only_reader(o.dst, i, i + 1) &&
+                only_reader(n1.dst, i + 1, i + 2) && only_reader(n2.dst, i + 2, i + 3) &&
+                clear_of(n3.dst, {o.src})) {
+                sp.rule = RULE_CA_MLP;
+                sp.out = n3.dst;
+                sp.last = i + 4;
+            }
+        }
+        // ChanScale -> Add: y = x * s + r in one pass.
+        if (sp.rule == RULE_NONE && o.kind == MX_OP_CHAN_SCALE && i + 1 < p->n_ops) {
+            const mx_op &n1 = p->ops[i + 1];
+            if (n1.kind == MX_OP_ADD && (n1.src == o.dst) != (n1.src2 == o.dst) && whole(n1, o.dst) &&
+                o.c * o.hw == n1.n && only_reader(o.dst, i, i + 1)) {
+                const int64_t r = n1.src == o.dst ? n1.src2 : n1.src;
+                if (clear_of(n1.dst, {o.src, o.src2, r})) {
+                    sp.rule = RULE_SCALE_ADD;
+                    sp.r1 = r;
+                    sp.out = n1.dst;
+                    sp.last = i + 2;
+                }
+            }
+        }
         // LayerNorm -> 1x1 conv: the conv's GEMM reads the LayerNorm's input
         // and normalises it on the way in (the streaming kernels' _ln form).
-        if (o.kind == MX_OP_CHAN_LN && i + 1 < p->n_ops) {
+        if (sp.rule == RULE_NONE && o.kind == MX_OP_CHAN_LN && i + 1 < p->n_ops) {
             const mx_op &n1 = p->ops[i + 1];
             if (n1.kind == MX_OP_CONV1X1 && n1.src == o.dst && n1.h * n1.wd == o.hw && o.hw > 1 &&
                 n1.c_in == o.c && o.hw % 4 == 0 && o.c % 16 == 0 && only_reader(o.dst, i, i + 1) &&
@@ -1114,7 +1145,7 @@ void Program::plan_fusion(const mx_plan_desc *p, bool require_clear) {
                 epilogue(i + 1, sp);
             }
         }
-        if (sp.ln < 0) epilogue(i, sp);
+        if (sp.rule == RULE_NONE && sp.ln < 0) epilogue(i, sp);
         fused_ops += sp.last - sp.first - 1;
         specs.push_back(sp);
         i = sp.last;
@@ -1241,6 +1272,29 @@ void Gpu::build_program(const mx_plan_desc *p) {
     };
     prog.clear();
     for (const StepSpec &sp : pg.specs) {
+        if (sp.rule == RULE_CA_MLP) {
+            GemvArgs g1, g2;
+            memcpy(&g1, ops[sp.first][0].a0, sizeof g1);
+            memcpy(&g2, ops[sp.first + 2][0].a0, sizeof g2);
+            CaArgs a{g1.x, g1.w, g1.bias, g2.w, g2.bias, dev(sp.out), g1.ci, g1.co, p->ops[sp.first + 1].slope, 0};
+            Launch l = mk("mx_ca_mlp");
+            set_args(l, a);
+            prog.push_back(Step{sp.first, sp.last, {l}});
+            continue;
+        }
+        if (sp.rule == RULE_SCALE_ADD) {
+            ChanScaleArgs a;
+            memcpy(&a, ops[sp.first][0].a0, sizeof a);
+            a.y = dev(sp.out);
+            a.r = dev(sp.r1);
+            const bool vec = a.hw % 4 == 0 && aligned(a.x, 16) && aligned(a.y, 16) && aligned(a.r, 16);
+            Launch l = mk(vec ? "mx_chan_scale_add_v4" : "mx_chan_scale_add_s");
+            l.g[0] = vec ? cdiv(a.hw / 4, MXK_BLOCK * 4) : cdiv(a.hw, MXK_BLOCK);
+            l.g[1] = grid_yz(a.c);
+            set_args(l, a);
+            prog.push_back(Step{sp.first, sp.last, {l}});
+            continue;
+        }
         if (sp.ln < 0) {
             if (sp.out < 0) prog.push_back(Step{sp.first, sp.last, ops[sp.first]});
             else prog.push_back(Step{sp.first, sp.last, {with_epilogue(sp, sp.first, ops[sp.first][0])}});

@@ -20,13 +20,25 @@ struct EwArgs {
     float slope;
 };
 
-// y[ch][p] = x[ch][p] * s[ch]
+// y[ch][p] = x[ch][p] * s[ch] (+ r[ch][p] when r is set: a residual add
+// fused into the scale)
 struct ChanScaleArgs {
     const float *x;
     const float *s;
     float *y;
     int64_t hw;
     int64_t c;
+    const float *r;
+};
+
+// The channel-attention MLP on a [c] vector, one block:
+// h = lrelu(b1 + W1 . x) ([r]), y = sigmoid(b2 + W2 . h) ([c]).
+struct CaArgs {
+    const float *x, *w1, *b1, *w2, *b2;
+    float *y;
+    int32_t c, r;
+    float slope;
+    int32_t pad;
 };
 
 // Channel LayerNorm over [c][hw].

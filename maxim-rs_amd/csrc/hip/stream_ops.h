@@ -97,6 +97,68 @@ extern "C" __global__ __launch_bounds__(MXK_BLOCK) void mx_chan_scale_s(ChanScal
     if (p < a.hw) a.y[ch * a.hw + p] = a.x[ch * a.hw + p] * a.s[ch];
 }
 
+// The CALayer's excitation and the residual add as one pass:
+// y = x * s[ch] + r, the two unfused kernels' operations in their order.
+extern "C" __global__ __launch_bounds__(MXK_BLOCK) void mx_chan_scale_add_v4(ChanScaleArgs a) {
+    const int64_t ch = blockIdx.y;
+    const float s = a.s[ch];
+    const float *x = a.x + ch * a.hw;
+    const float *r = a.r + ch * a.hw;
+    float *y = a.y + ch * a.hw;
+    const int64_t nv = a.hw >> 2;
+    float4 v[4], w[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+        const int64_t j = (int64_t)blockIdx.x * (MXK_BLOCK * 4) + u * MXK_BLOCK + threadIdx.x;
+        if (j < nv) {
+            v[u] = ld4(x + 4 * j);
+            w[u] = ld4(r + 4 * j);
+        }
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+        const int64_t j = (int64_t)blockIdx.x * (MXK_BLOCK * 4) + u * MXK_BLOCK + threadIdx.x;
+        if (j < nv) {
+            float4 t = v[u];
+            t.x = t.x * s + w[u].x;
+            t.y = t.y * s + w[u].y;
+            t.z = t.z * s + w[u].z;
+            t.w = t.w * s + w[u].w;
+            st4(y + 4 * j, t);
+        }
+    }
+}
+
+extern "C" __global__ __launch_bounds__(MXK_BLOCK) void mx_chan_scale_add_s(ChanScaleArgs a) {
+    const int64_t ch = blockIdx.y;
+    int64_t p = (int64_t)blockIdx.x * MXK_BLOCK + threadIdx.x;
+    if (p < a.hw) {
+        const int64_t i = ch * a.hw + p;
+        a.y[i] = a.x[i] * a.s[ch] + a.r[i];
+    }
+}
+
+// The channel-attention MLP (CALayer, two plane-1 1x1 convs around a leaky
+// ReLU, then the sigmoid) in one block, with mx_gemv's summation order (bias
+// first, inputs ascending) and the elementwise kernels' expressions, so the
+// result is that of the four unfused launches to the bit.
+extern "C" __global__ __launch_bounds__(MXK_BLOCK) void mx_ca_mlp(CaArgs a) {
+    __shared__ float h[1024];
+    for (int j = threadIdx.x; j < a.r; j += MXK_BLOCK) {
+        const float *w = a.w1 + (int64_t)j * a.c;
+        float acc = a.b1 ? a.b1[j] : 0.0f;
+        for (int i = 0; i < a.c; ++i) acc += w[i] * a.x[i];
+        h[j] = acc >= 0.0f ? acc : a.slope * acc;
+    }
+    __syncthreads();
+    for (int o = threadIdx.x; o < a.c; o += MXK_BLOCK) {
+        const float *w = a.w2 + (int64_t)o * a.r;
+        float acc = a.b2 ? a.b2[o] : 0.0f;
+        for (int j = 0; j < a.r; ++j) acc += w[j] * h[j];
+        a.y[o] = 1.0f / (1.0f + expf(-acc));
+    }
+}
+
 // ------------------------------------------------------------ LayerNorm
 //
 // Per pixel: s1, s2 in ascending channel order, m = s1/c, var = s2/c - m*m,
