@@ -67,6 +67,10 @@ void mxh_set_fusion(mxh_gpu *g, int on);
  * plan's own layout. */
 int mxh_plan_program(const mx_plan_desc *plan, int repack, uint64_t *fused_ops, uint64_t *arena_len,
                      uint64_t *offs, uint64_t *step_first, uint64_t *step_last, uint64_t *n_steps);
+/* Which buffer owns each buffer's storage in that device layout (n_bufs
+ * entries): a view's base, the buffer itself, or - for the source of a copy
+ * the executor elides - the copy destination's owner. */
+int mxh_plan_storage(const mx_plan_desc *plan, int repack, int64_t *owner);
 uint64_t mxh_fused_ops(mxh_gpu *g);
 uint64_t mxh_steps(mxh_gpu *g);
 int mxh_step_info(mxh_gpu *g, uint64_t i, uint64_t *first, uint64_t *last, const char **kernel);

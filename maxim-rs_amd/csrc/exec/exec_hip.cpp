@@ -202,7 +202,7 @@ std::string conv_name(ConvCfg c, bool k3) {
 
 // What the executor decides about a plan before touching the device: which
 // ops fuse into which steps, and where every buffer lives in the device arena.
-enum { RULE_NONE = 0, RULE_CA_MLP = 1, RULE_SCALE_ADD = 2 };
+enum { RULE_NONE = 0, RULE_CA_MLP = 1, RULE_SCALE_ADD = 2, RULE_ELIDED = 3 };
 
 struct StepSpec {
     uint64_t first = 0, last = 0;
@@ -215,7 +215,9 @@ struct StepSpec {
 
 struct Program {
     std::vector<StepSpec> specs;
-    std::vector<uint64_t> doff;  // device element offset of every buffer
+    std::vector<int64_t> elide_to;  // x -> the copy destination whose storage x takes, or -1
+    std::vector<int64_t> dbase;     // the buffer that owns each buffer's device storage
+    std::vector<uint64_t> doff;     // device element offset of every buffer
     uint64_t arena_len = 0;
     uint64_t fused_ops = 0;
     bool repacked = false;
@@ -1098,6 +1100,64 @@ void Program::plan_fusion(const mx_plan_desc *p, bool require_clear) {
         }
     };
 
+    // Copy elision (own device layout only): a copy whose source x has one
+    // writer and no other reader, and whose destination's bytes nothing
+    // touches between that writer and the copy, is served by laying x out on
+    // the destination's storage: the writer then produces the destination
+    // directly and the copy's step launches nothing (run op by op it copies
+    // the destination onto itself). Checked per storage owner (the view
+    // table's base), since the executor lays out every owner itself.
+    elide_to.assign(p->n_bufs, -1);
+    std::vector<char> elided(p->n_ops, 0);
+    if (!require_clear) {
+        const uint64_t nb = p->n_bufs;
+        std::vector<int64_t> base(nb);
+        std::vector<uint64_t> delta(nb);
+        std::vector<int> views(nb, 0), writers(nb, 0);
+        std::vector<char> target(nb, 0);
+        for (uint64_t b = 0; b < nb; ++b) {
+            const int64_t par = p->alias_parent[b];
+            base[b] = par < 0 ? (int64_t)b : base[par];
+            delta[b] = par < 0 ? 0 : delta[par] + p->alias_delta[b];
+            if (par >= 0) ++views[base[b]];
+        }
+        for (uint64_t k = 0; k < p->n_ops; ++k)
+            for (int64_t d : writes_of(p->ops[k])) ++writers[d];
+        auto blen = [&](int64_t b) { return (uint64_t)(p->bufs[b].c * p->bufs[b].h * p->bufs[b].w); };
+        auto shares = [&](int64_t b, int64_t d) {
+            return base[b] == base[d] && delta[b] < delta[d] + blen(d) && delta[d] < delta[b] + blen(b);
+        };
+        auto touches = [&](const mx_op &o, int64_t d) {
+            for (int64_t b : reads_of(o))
+                if (shares(b, d)) return true;
+            for (int64_t b : writes_of(o))
+                if (shares(b, d)) return true;
+            return false;
+        };
+        for (uint64_t j = 0; j < p->n_ops; ++j) {
+            const mx_op &c = p->ops[j];
+            if (c.kind != MX_OP_COPY) continue;
+            const int64_t x = c.src, d = c.dst;
+            if (x == d || base[x] != x || views[x] || writers[x] != 1 || target[x] || elide_to[d] >= 0) continue;
+            if ((uint64_t)x == p->input || (uint64_t)x == p->output || (p->keep && p->keep[x])) continue;
+            if ((uint64_t)c.n != blen(x) || (uint64_t)c.n != blen(d)) continue;
+            int64_t w = -1;  // x's writer
+            for (uint64_t k = 0; k < j; ++k)
+                for (int64_t b : writes_of(p->ops[k]))
+                    if (b == x) w = (int64_t)k;
+            if (w < 0 || !only_reader(x, (uint64_t)w, j)) continue;
+            bool ok = true;
+            for (uint64_t k = 0; k < (uint64_t)w && ok; ++k)  // nothing reads x before it is written
+                for (int64_t b : reads_of(p->ops[k])) ok = ok && b != x;
+            for (int64_t b : reads_of(p->ops[w])) ok = ok && !shares(b, d);  // the writer reads no byte of d
+            for (uint64_t k = (uint64_t)w + 1; k < j && ok; ++k) ok = !touches(p->ops[k], d);
+            if (!ok) continue;
+            elide_to[x] = d;
+            target[d] = 1;
+            elided[j] = 1;
+        }
+    }
+
     specs.clear();
     fused_ops = 0;
     for (uint64_t i = 0; i < p->n_ops;) {
@@ -1105,6 +1165,13 @@ void Program::plan_fusion(const mx_plan_desc *p, bool require_clear) {
         StepSpec sp;
         sp.first = i;
         sp.last = i + 1;
+        if (elided[i]) {
+            sp.rule = RULE_ELIDED;
+            ++fused_ops;
+            specs.push_back(sp);
+            ++i;
+            continue;
+        }
         // The CALayer's MLP: plane-1 Conv1x1 -> Lrelu -> plane-1 Conv1x1 ->
         // Sigmoid, one block (mx_ca_mlp).
         if (o.kind == MX_OP_CONV1X1 && o.h * o.wd == 1 && i + 3 < p->n_ops && o.c_out <= 1024) {
@@ -1161,8 +1228,15 @@ void Program::plan_fusion(const mx_plan_desc *p, bool require_clear) {
 void Program::layout(const mx_plan_desc *p, bool repack) {
     const uint64_t n = p->n_bufs;
     doff.assign(n, 0);
+    dbase.assign(n, 0);
     if (!repack) {
-        for (uint64_t i = 0; i < n; ++i) doff[i] = p->offs[i];
+        for (uint64_t i = 0; i < n; ++i) {
+            doff[i] = p->offs[i];
+            dbase[i] = (int64_t)i;
+        }
+        if (p->alias_parent)
+            for (uint64_t i = 0; i < n; ++i)
+                if (p->alias_parent[i] >= 0) dbase[i] = dbase[p->alias_parent[i]];
         arena_len = p->arena_len;
         return;
     }
@@ -1177,6 +1251,13 @@ void Program::layout(const mx_plan_desc *p, bool repack) {
             delta[i] = delta[par] + p->alias_delta[i];
         }
     }
+    // an elided copy's source takes its destination's storage
+    for (uint64_t i = 0; i < n; ++i)
+        if (i < elide_to.size() && elide_to[i] >= 0) {
+            base[i] = base[elide_to[i]];
+            delta[i] = delta[elide_to[i]];
+        }
+    for (uint64_t i = 0; i < n; ++i) dbase[i] = base[i];
     const uint64_t DEAD = UINT64_MAX;
     std::vector<uint64_t> first(n, DEAD), last(n, 0);
     for (uint64_t s = 0; s < specs.size(); ++s)
@@ -1272,6 +1353,10 @@ void Gpu::build_program(const mx_plan_desc *p) {
     };
     prog.clear();
     for (const StepSpec &sp : pg.specs) {
+        if (sp.rule == RULE_ELIDED) {
+            prog.push_back(Step{sp.first, sp.last, {}});
+            continue;
+        }
         if (sp.rule == RULE_CA_MLP) {
             GemvArgs g1, g2;
             memcpy(&g1, ops[sp.first][0].a0, sizeof g1);
@@ -1489,6 +1574,16 @@ int mxh_plan_program(const mx_plan_desc *plan, int repack, uint64_t *fused_ops, 
             if (step_first) step_first[i] = pg.specs[i].first;
             if (step_last) step_last[i] = pg.specs[i].last;
         }
+    });
+}
+
+int mxh_plan_storage(const mx_plan_desc *plan, int repack, int64_t *owner) {
+    return guard([&] {
+        mxh::Program pg;
+        const bool rp = repack && plan->alias_parent && plan->alias_delta;
+        pg.plan_fusion(plan, !rp);
+        pg.layout(plan, rp);
+        if (owner) memcpy(owner, pg.dbase.data(), sizeof(int64_t) * pg.dbase.size());
     });
 }
 
