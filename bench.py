@@ -9,9 +9,9 @@ in HBM when the timed region starts. Prints ONE JSON line:
   ms_per_step   ms/image
   roofline      the dominant kernel's achieved rate against its bound (fp32
                 MFMA 157.3 TFLOP/s or HBM 8 TB/s): algorithmic FLOPs or bytes
-                per launch over the average launch duration, from HIP events
-                around every step on the executor's stream over K further
-                (eager) passes
+                per launch over the average launch duration, from the HIP
+                start/stop events each dispatch records on the executor's
+                stream over K further (eager) passes
   cpu_baseline  the CPU path (oracle/, a C restatement of the reference's
                 src/exec_cpu.rs) timed on this host over one full pass
 
@@ -51,7 +51,7 @@ def smooth_image(h, w, seed=0, noise=0.1):
 
 def family(kernel):
     """Group kernel entry points into the family a roofline is quoted for."""
-    for pre in ("mx_gemm", "mx_conv3x3", "mx_conv4x4", "mx_chan_ln", "mx_block_perm", "mx_resize",
+    for pre in ("mx_gemm", "mx_pw", "mx_conv3x3", "mx_conv4x4", "mx_chan_ln", "mx_block_perm", "mx_resize",
                 "mx_chan_mean", "mx_gemv"):
         if kernel.startswith(pre):
             return pre
@@ -64,6 +64,9 @@ def main():
     ap.add_argument("--steps", type=int, default=30)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--eager", action="store_true",
+                    help="time eager launches of the fused program instead of graph replays "
+                         "(the same kernels; for tracing tools)")
     ap.add_argument("--cpu-threads", type=int, default=min(16, os.cpu_count() or 1))
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -90,40 +93,41 @@ def main():
     out = gpu.run(pad.img)
     e2e_first = time.perf_counter() - t0
     assert np.isfinite(out).all(), "non-finite output"
+    n_ops_all = len(plan.ops)
+    one_pass = (lambda: gpu.run_ops(0, n_ops_all)) if args.eager else gpu.run_graph
     for _ in range(args.warmup):
-        gpu.run_graph()
+        one_pass()
     gpu.sync()
 
     # Timed region: K passes over the resident image, each one replay of the
-    # captured graph of the fused program (the executor's serving path),
-    # bracketed by device synchronisation.
+    # captured graph of the fused program (the executor's serving path; with
+    # --eager the same launches issued one by one), bracketed by device
+    # synchronisation.
     gpu.sync()
     t_start = time.perf_counter()
     for _ in range(args.steps):
-        gpu.run_graph()
+        one_pass()
     gpu.sync()
     wall = time.perf_counter() - t_start
     ms_per_step = wall * 1e3 / args.steps
 
-    # Attribution: K more passes of the same program launched eagerly with a
-    # HIP event pair around every step on the executor's stream. A fused
-    # step is charged its ops' FLOPs and their compulsory bytes less the
-    # intermediate it no longer writes and reads back.
+    # Attribution: K more passes of the same program launched eagerly, each
+    # launch timed by the start/stop events its dispatch records on the
+    # executor's stream. Each launch is charged its kernel's algorithmic cost
+    # (launch_costs).
     steps = gpu.steps()
-    cost = []
-    for a, b, kn in steps:
-        f = sum(R.op_cost(plan.ops[k])[0] for k in range(a, b))
-        by = sum(R.op_cost(plan.ops[k])[1] for k in range(a, b))
-        by -= sum(8 * plan.buf_len(plan.ops[k].dst) for k in range(a, b - 1))
-        cost.append((kn, f, by))
+    launches = gpu.launches()
+    cost = launch_costs(plan, steps, launches, R)
     per_kernel = collections.defaultdict(lambda: [0.0, 0, 0.0, 0.0])  # ms, launches, flops, bytes
     ev_tot = []
     for _ in range(args.steps):
-        per, tot = gpu.run_timed()
+        _, tot = gpu.run_timed()
         ev_tot.append(tot)
-        for si, (kn, f, by) in enumerate(cost):
+        ms = gpu.launch_timeline()
+        for k, (st, kn) in enumerate(launches):
+            f, by = cost[k]
             e = per_kernel[kn]
-            e[0] += float(per[si])
+            e[0] += float(ms[k])
             e[1] += 1
             e[2] += f
             e[3] += by
@@ -146,8 +150,9 @@ def main():
     roof["algorithmic_per_launch"] = {"gflop": fl / nl / 1e9, "mb": by / nl / 1e6}
 
     fl_all, by_all, bound_s = R.plan_cost(plan)
-    print("bench: %.3f ms/image (graph replays), %.3f ms event-timed eager pass, %d steps for %d ops; "
-          "roofline sum of per-op bounds %.2f ms" % (ms_per_step, ev_ms, len(steps), n_ops, bound_s * 1e3),
+    print("bench: %.3f ms/image (%s), %.3f ms event-timed eager pass, %d steps for %d ops; "
+          "roofline sum of per-op bounds %.2f ms" % (ms_per_step, "eager launches" if args.eager else "graph replays",
+                                                      ev_ms, len(steps), n_ops, bound_s * 1e3),
           file=sys.stderr)
     print("bench: first pass incl. H2D/D2H and launch setup %.1f ms" % (e2e_first * 1e3), file=sys.stderr)
     fams = collections.defaultdict(lambda: [0.0, 0])
@@ -181,13 +186,59 @@ def main():
         "dtype": "fp32",
         "data": "synthetic: seeded He-normal x0.3 weights, 600x400 smooth pattern + N(0,0.1) image",
         "config": {"workload": "C4: MAXIM-3S, 600x400 RGB reflect-padded to 640x448, one image per step",
-                   "variant": "S-3", "ops": n_ops, "arena_mib": round(plan.arena_bytes / 2**20, 1),
+                   "variant": "S-3", "ops": n_ops, "launch": "eager" if args.eager else "graph", "arena_mib": round(plan.arena_bytes / 2**20, 1),
                    "gflop_per_image": round(fl_all / 1e9, 1), "gb_per_image": round(by_all / 1e9, 2),
                    "sum_of_op_bounds_ms": round(bound_s * 1e3, 2)},
         "roofline": roof,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)
+
+
+def launch_costs(plan, steps, launches, R):
+    """(flops, bytes) of every launch: FLOPs = 2 x MACs; bytes = what the
+    kernel must move (inputs once, output once, weights once). A step of one
+    launch is charged its ops' costs less the intermediates it no longer
+    writes and reads back; the steps of several launches are split by kernel:
+    a folded LayerNorm's statistics pass (reads x, writes mean and 1/std) and
+    the GEMM that re-reads x with them, the two resize passes through `tmp`,
+    and the channel mean's partial and final sums."""
+    def step_cost(a, b):
+        f = sum(R.op_cost(plan.ops[k])[0] for k in range(a, b))
+        by = sum(R.op_cost(plan.ops[k])[1] for k in range(a, b))
+        by -= sum(8 * plan.buf_len(plan.ops[k].dst) for k in range(a, b - 1))
+        return f, by
+
+    per_step = collections.defaultdict(list)
+    for i, (st, kn) in enumerate(launches):
+        per_step[st].append(i)
+    out = [None] * len(launches)
+    for st, idx in per_step.items():
+        a, b, _ = steps[st]
+        o = plan.ops[a]
+        names = [launches[i][1] for i in idx]
+        if len(idx) == 1:
+            out[idx[0]] = step_cost(a, b)
+            continue
+        for i, kn in zip(idx, names):
+            if kn.startswith("mx_chan_ln_stats"):
+                out[i] = (0, 4 * (o.c * o.hw + 2 * o.hw))
+            elif kn.startswith("mx_pw_") and "_ln" in kn:
+                f, by = step_cost(a, b)
+                out[i] = (f, by + 8 * o.hw)  # + the statistics it reads
+            elif kn.startswith("mx_chan_ln"):  # a LayerNorm that could not be folded
+                out[i] = R.op_cost(o)
+            elif kn == "mx_resize_h":
+                out[i] = (0, 4 * (o.c * o.h * o.wd + o.c * o.h * o.ow))
+            elif kn == "mx_resize_v":
+                out[i] = (0, 4 * (o.c * o.h * o.ow + o.c * o.oh * o.ow))
+            elif kn == "mx_chan_mean_part":
+                out[i] = (0, 4 * o.c * o.hw)
+            elif kn == "mx_chan_mean_final":
+                out[i] = (0, 4 * o.c)
+            else:  # the GEMM after an unfolded LayerNorm
+                out[i] = step_cost(a + 1, b)
+    return out
 
 
 def cpu_baseline(plan, img, threads):

@@ -105,8 +105,19 @@ int mxh_sync(mxh_gpu *g);
 void mxh_set_timeline(mxh_gpu *g, int on);
 int mxh_timeline(mxh_gpu *g, float *per_step_ms, uint64_t n, float *total_ms);
 /* Gpu::run_timed (src/exec_gpu.rs:241-265) without the copies: every op over
- * the image already in the arena, one event per op, one synchronisation. */
+ * the image already in the arena, every launch timed by its dispatch, one
+ * synchronisation. */
 int mxh_run_timed(mxh_gpu *g, const mx_plan_desc *plan);
+
+/* The launches of the current program (fused steps with fusion on, ops
+ * with it off), in order: how many, each one's step (or op) and kernel, and -
+ * after mxh_run_timed - each one's device milliseconds, from the start/stop
+ * events the dispatch itself records (hipExtModuleLaunchKernel: the kernel's
+ * execution, not the gap before it). A step's entry in mxh_timeline is the
+ * sum over its launches. */
+uint64_t mxh_launches(mxh_gpu *g);
+int mxh_launch_info(mxh_gpu *g, uint64_t i, uint64_t *step, const char **kernel);
+int mxh_launch_timeline(mxh_gpu *g, float *ms, uint64_t n);
 
 /* Time `iters` passes of ops [first, last) back to back with HIP events on
  * the executor's stream; `ms` gets the total device time. */

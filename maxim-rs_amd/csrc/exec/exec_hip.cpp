@@ -317,26 +317,48 @@ public:
     // All ops with an event before each and one after the last; one sync.
     // Every step (one op, or one fused launch standing for several) with an
     // event before each and one after the last; one synchronisation.
+    // Every launch of the program (fused steps, or ops with fusion off) in
+    // order, with the step or op it belongs to.
+    std::vector<std::pair<uint64_t, const Launch *>> launch_list() const {
+        std::vector<std::pair<uint64_t, const Launch *>> v;
+        const uint64_t n = fusion ? prog.size() : n_ops;
+        for (uint64_t i = 0; i < n; ++i)
+            for (const Launch &l : fusion ? prog[i].launches : ops[i]) v.push_back({i, &l});
+        return v;
+    }
+    // Every launch timed by the dispatch itself (hipExtModuleLaunchKernel's
+    // start/stop events bracket the kernel's execution, not the gap before
+    // it), one synchronisation: per-launch and per-step (the sum of its
+    // launches) device milliseconds.
     void run_timed() {
         const uint64_t n = fusion ? prog.size() : n_ops;
-        std::vector<hipEvent_t> ev(n + 1);
+        const auto seq = launch_list();
+        std::vector<hipEvent_t> ev(2 * seq.size());
         for (auto &e : ev) check(H.hipEventCreate(&e), "hipEventCreate");
-        for (uint64_t i = 0; i < n; ++i) {
-            check(H.hipEventRecord(ev[i], stream), "hipEventRecord");
-            if (fusion) run_range(prog[i].first, prog[i].last);
-            else run_op(i);
+        for (size_t k = 0; k < seq.size(); ++k) {
+            Launch &l = const_cast<Launch &>(*seq[k].second);
+            void *params[2] = {l.a0, l.a1};
+            const uint64_t gx = (uint64_t)l.g[0] * l.b[0], gy = (uint64_t)l.g[1] * l.b[1], gz = (uint64_t)l.g[2] * l.b[2];
+            if (gx > 0xffffffffULL || gy > 0xffffffffULL || gz > 0xffffffffULL) throw Error("a timed launch exceeds 2^32 work-items");
+            check(H.hipExtModuleLaunchKernel(l.f, (uint32_t)gx, (uint32_t)gy, (uint32_t)gz, l.b[0], l.b[1], l.b[2], 0,
+                                             stream, params, nullptr, ev[2 * k], ev[2 * k + 1], 0),
+                  l.name);
+            ++kernels;
         }
-        check(H.hipEventRecord(ev[n], stream), "hipEventRecord");
+        for (uint64_t i = 0; i < n; ++i) launched += fusion ? prog[i].last - prog[i].first : 1;
         sync();
         per_op_ms.assign(n, 0.0f);
+        per_launch_ms.assign(seq.size(), 0.0f);
         total_ms = 0.0f;
-        for (uint64_t i = 0; i < n; ++i) {
-            check(H.hipEventElapsedTime(&per_op_ms[i], ev[i], ev[i + 1]), "hipEventElapsedTime");
-            total_ms += per_op_ms[i];
+        for (size_t k = 0; k < seq.size(); ++k) {
+            check(H.hipEventElapsedTime(&per_launch_ms[k], ev[2 * k], ev[2 * k + 1]), "hipEventElapsedTime");
+            per_op_ms[seq[k].first] += per_launch_ms[k];
+            total_ms += per_launch_ms[k];
         }
         for (auto &e : ev) H.hipEventDestroy(e);
         have_timeline = true;
     }
+    std::vector<float> per_launch_ms;
     void write(uint64_t off, const float *v, uint64_t n) {
         if (n == 0) return;
         if (off + n > arena_len) throw Error("a write of " + std::to_string(n) + " floats at " + std::to_string(off) + " runs past the arena");
@@ -1668,6 +1690,26 @@ int mxh_sync(mxh_gpu *g) {
 }
 
 void mxh_set_timeline(mxh_gpu *g, int on) { G(g)->want_timeline = on != 0; }
+
+uint64_t mxh_launches(mxh_gpu *g) { return G(g)->launch_list().size(); }
+
+int mxh_launch_info(mxh_gpu *g, uint64_t i, uint64_t *step, const char **kernel) {
+    return guard([&] {
+        const auto seq = G(g)->launch_list();
+        if (i >= seq.size()) throw mx::Error("launch index out of range");
+        if (step) *step = seq[i].first;
+        if (kernel) *kernel = seq[i].second->name;
+    });
+}
+
+int mxh_launch_timeline(mxh_gpu *g, float *ms, uint64_t n) {
+    return guard([&] {
+        Gpu &x = *G(g);
+        if (!x.have_timeline) throw mx::Error("no timeline recorded (mxh_run_timed)");
+        if (n != x.per_launch_ms.size()) throw mx::Error("launch_timeline: wrong length");
+        if (ms) memcpy(ms, x.per_launch_ms.data(), sizeof(float) * n);
+    });
+}
 
 int mxh_timeline(mxh_gpu *g, float *per_op_ms, uint64_t n, float *total_ms) {
     return guard([&] {

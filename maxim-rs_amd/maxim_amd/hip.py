@@ -50,6 +50,9 @@ def _lib():
             "mxh_step_info": (I, [V, U, C.POINTER(C.c_uint64), C.POINTER(C.c_uint64),
                                   C.POINTER(C.c_char_p)]),
             "mxh_time_ops": (I, [V, D, U, U, I, C.POINTER(C.c_float)]),
+            "mxh_launches": (U, [V]),
+            "mxh_launch_info": (I, [V, U, C.POINTER(C.c_uint64), C.POINTER(C.c_char_p)]),
+            "mxh_launch_timeline": (I, [V, V, U]),
             "mxh_device_name": (C.c_char_p, [V]),
             "mxh_arena_bytes": (U, [V]),
             "mxh_weight_bytes": (U, [V]),
@@ -186,6 +189,23 @@ class Gpu:
         """Every step over the resident input, one event per step: (per-step ms, total ms)."""
         _check(_lib().mxh_run_timed(self._h, self._d))
         return self.timeline()
+
+    def launches(self):
+        """[(step, kernel)] of every launch of the current program, in order."""
+        L = _lib()
+        out = []
+        st, k = C.c_uint64(), C.c_char_p()
+        for i in range(L.mxh_launches(self._h)):
+            _check(L.mxh_launch_info(self._h, i, C.byref(st), C.byref(k)))
+            out.append((st.value, k.value.decode()))
+        return out
+
+    def launch_timeline(self):
+        """Per-launch device ms of the last run_timed()."""
+        n = _lib().mxh_launches(self._h)
+        ms = np.empty(n, np.float32)
+        _check(_lib().mxh_launch_timeline(self._h, ms.ctypes.data, n))
+        return ms
 
     def time_ops(self, first, last, iters=1):
         ms = C.c_float()

@@ -109,6 +109,17 @@ def test_timeline_and_counters(gpu_ok):
     gpu.run(smooth_image(64, 64))
     per, total = gpu.timeline()
     assert per.shape == (len(steps),)
+    # per-launch events: every launch names its step, and a step's time is
+    # the sum of its launches'
+    per, total = gpu.run_timed()
+    launches = gpu.launches()
+    ms = gpu.launch_timeline()
+    assert len(launches) == len(ms) and all(0 <= st < len(steps) for st, _ in launches)
+    assert [st for st, _ in launches] == sorted(st for st, _ in launches)
+    sums = np.zeros(len(steps))
+    for (st, _), t in zip(launches, ms):
+        sums[st] += t
+    assert np.allclose(sums, per, rtol=1e-5, atol=1e-6) and abs(ms.sum() - total) < 1e-3 * total + 1e-3
 
 
 @pytest.mark.parametrize("variant,side", [("S-2", 128), ("S-3", 64)])
