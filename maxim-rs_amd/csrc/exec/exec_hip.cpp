@@ -169,7 +169,16 @@ std::string gemm_name(Tile t, bool vec) {
 // Same cost model as the GEMM tile.
 struct ConvCfg {
     int bm = 0, th = 0, ck = 0;
+    int c3bm = 0, c3th = 0;  // the mx_c3 tile, when the op qualifies for it
 };
+
+// The mx_c3 tile (c_in % 16 == 0 and >= 128, width % 4 == 0; measured
+// faster than the implicit-GEMM kernel there, slower below): 64 output
+// channels x 4 rows, or 32 x 8 for narrow outputs.
+void pick_c3(ConvCfg &c, int64_t co) {
+    c.c3bm = co >= 64 ? 64 : 32;
+    c.c3th = co >= 64 ? 4 : 8;
+}
 
 ConvCfg pick_conv(int64_t co, int64_t ci, int64_t oh, int64_t ow, bool k3, int cus) {
     static const struct {
@@ -190,6 +199,13 @@ ConvCfg pick_conv(int64_t co, int64_t ci, int64_t oh, int64_t ow, bool k3, int c
         }
     }
     r.ck = (k3 && ci > 4) ? 8 : 4;
+    if (k3 && ci > 4) {
+        // measured on MI355X at the MAXIM shapes (c -> c, 32 to 128 channels):
+        // 32-channel blocks of 8 rows for narrow outputs, 64 x 4 up to 64
+        // channels, 32 x 4 beyond (the grid-filling shapes win)
+        r.bm = co <= 32 ? 32 : co <= 64 ? 64 : 32;
+        r.th = co <= 32 ? 8 : 4;
+    }
     return r;
 }
 
@@ -609,6 +625,23 @@ Gpu::Gpu(const mx_plan_desc *p) : H(hip()), doff(pg.doff) {
                                     t[((mb * nch + ch) * kc + k) * cc.bm + m] = w[(gm * o.c_in + gc) * taps + tp];
                             }
                 extra[i][0] = placev(t);
+                if (k3 && o.c_in % 16 == 0 && o.c_in >= 128 && o.wd % 4 == 0) {
+                    // the mx_c3 weight tiles: [m-block][chunk][BM][tap][16]
+                    pick_c3(ccfg[i], o.c_out);
+                    const int bm = ccfg[i].c3bm;
+                    const int64_t nb = (o.c_out + bm - 1) / bm, nc = o.c_in / 16;
+                    std::vector<float> u((size_t)(nb * nc * bm * 9 * 16), 0.0f);
+                    for (int64_t mb = 0; mb < nb; ++mb)
+                        for (int64_t ch = 0; ch < nc; ++ch)
+                            for (int64_t m = 0; m < bm; ++m)
+                                for (int tp = 0; tp < 9; ++tp)
+                                    for (int c = 0; c < 16; ++c) {
+                                        const int64_t gm = mb * bm + m, gc = ch * 16 + c;
+                                        if (gm < o.c_out)
+                                            u[(((mb * nc + ch) * bm + m) * 9 + tp) * 16 + c] = w[(gm * o.c_in + gc) * 9 + tp];
+                                    }
+                    extra[i][1] = placev(u);
+                }
                 as_is(o.bias);
                 break;
             }
@@ -844,7 +877,20 @@ void Gpu::build_launches(const mx_plan_desc *p, const std::vector<int64_t> &woff
                 l.g[1] = grid_yz((o.c_out + cc.bm - 1) / cc.bm);
                 set_args(l, a);
                 l.kind = 2;
-                L.push_back(l);
+                if (k3 && extra[i][1] >= 0 && aligned(a.x, 16) && aligned(a.y, 16)) {
+                    // mx_c3 (channel-last LDS tiles, 128-bit fragment reads)
+                    ConvArgs b = a;
+                    b.w = X(i, 1);
+                    Launch q = mk("mx_c3_m" + std::to_string(cc.c3bm) + "_t" + std::to_string(cc.c3th));
+                    q.g[0] = cdiv((int64_t)((a.oh + cc.c3th - 1) / cc.c3th) * ((a.ow + 15) / 16), 1);
+                    q.g[1] = grid_yz((o.c_out + cc.c3bm - 1) / cc.c3bm);
+                    set_args(q, b);
+                    q.kind = 2;
+                    alt[i].push_back(l);
+                    L.push_back(q);
+                } else {
+                    L.push_back(l);
+                }
                 break;
             }
             case MX_OP_CONVT2X2: {
@@ -1352,6 +1398,7 @@ void Gpu::build_program(const mx_plan_desc *p) {
         Launch l = base;
         if (!strncmp(l.name, "mx_pw_", 6) && !(ealign && aligned(dev(sp.out), 16)))
             l = alt[g][0];  // the streaming kernels store 128 bits at a time
+        if (!strncmp(l.name, "mx_c3_", 6) && !aligned(dev(sp.out), 16)) l = alt[g][0];  // so does mx_c3
         l.name = intern(std::string(l.name) + "_f");
         l.f = fn(l.name);
         if (l.kind == 1) {

@@ -3,4 +3,5 @@
 #include "stream_ops.h"
 #include "gemm.h"
 #include "conv.h"
+#include "conv3.h"
 #include "pointwise.h"
