@@ -224,6 +224,8 @@ struct StepSpec {
     uint64_t first = 0, last = 0;
     int rule = RULE_NONE;  // a fusion that is not a producer's epilogue
     int64_t ln = -1;  // a LayerNorm op folded into the next op's GEMM (== first)
+    bool epi = false;  // the producer applies readers in its epilogue
+    int64_t perm = -1, pout = -1;  // a BlockPerm folded into the stores, and its source
     int64_t out = -1, u = -1, r1 = -1, r2 = -1;
     int act = MXK_ACT_NONE;
     float slope = 0.0f;
@@ -1164,8 +1166,32 @@ void Program::plan_fusion(const mx_plan_desc *p, bool require_clear) {
         if (f.out >= 0) {
             for (int64_t r : {f.u, f.r1, f.r2})
                 if (r >= 0) reads.push_back(r);
+            f.epi = true;
             if (clear_of(f.out, reads)) sp = f;
         }
+    };
+    // A backward BlockPerm (no swap, full coverage) of a GEMM step's output:
+    // the streaming kernels' stores go straight to the image positions.
+    auto perm_out = [&](uint64_t g, StepSpec &sp) {
+        const mx_op &o = p->ops[g];
+        if (!gemm_op(o) || sp.last >= p->n_ops) return;
+        const int64_t x = sp.out >= 0 ? sp.out : o.dst;
+        const uint64_t j = sp.last;
+        const mx_op &q = p->ops[j];
+        if (q.kind != MX_OP_BLOCK_PERM || q.src != x || (q.mode & (MX_PERM_SWAP | MX_PERM_FORWARD))) return;
+        const int64_t gh = q.p[0], gw = q.p[1], fh = q.p[2], fw = q.p[3];
+        const uint64_t n = (uint64_t)(q.c * q.h * q.wd);
+        if (gh * fh != q.h || gw * fw != q.wd || fw % 4 || range(x).b - range(x).a != n || n >= (1ULL << 31)) return;
+        if (!only_reader(x, j - 1, j)) return;
+        std::vector<int64_t> reads = reads_of(o);
+        if (sp.ln >= 0) reads.push_back(p->ops[sp.ln].src);
+        for (int64_t r : {sp.u, sp.r1, sp.r2})
+            if (r >= 0) reads.push_back(r);
+        if (!clear_of(q.dst, reads)) return;
+        sp.pout = x;
+        sp.perm = (int64_t)j;
+        sp.out = q.dst;
+        sp.last = j + 1;
     };
 
     // Copy elision (own device layout only): a copy whose source x has one
@@ -1278,9 +1304,13 @@ void Program::plan_fusion(const mx_plan_desc *p, bool require_clear) {
                 sp.ln = (int64_t)i;
                 sp.last = i + 2;
                 epilogue(i + 1, sp);
+                perm_out(i + 1, sp);
             }
         }
-        if (sp.rule == RULE_NONE && sp.ln < 0) epilogue(i, sp);
+        if (sp.rule == RULE_NONE && sp.ln < 0) {
+            epilogue(i, sp);
+            perm_out(i, sp);
+        }
         fused_ops += sp.last - sp.first - 1;
         specs.push_back(sp);
         i = sp.last;
@@ -1384,8 +1414,9 @@ void Program::layout(const mx_plan_desc *p, bool repack) {
 // step is the producer's launch with its destination and epilogue patched.
 void Gpu::build_program(const mx_plan_desc *p) {
     auto dev = [&](int64_t id) -> float * { return id >= 0 ? arena + doff[id] : nullptr; };
-    // The producer g's launch with the step's epilogue applied (kernel + _f).
-    auto with_epilogue = [&](const StepSpec &sp, uint64_t g, const Launch &base) {
+    // The producer g's launch with the step's epilogue applied (kernel + _f),
+    // writing buffer `out`.
+    auto with_epilogue = [&](const StepSpec &sp, uint64_t g, const Launch &base, int64_t out) {
         Epilogue e{};
         e.u = dev(sp.u);
         e.r1 = dev(sp.r1);
@@ -1396,22 +1427,22 @@ void Gpu::build_program(const mx_plan_desc *p) {
         // output on a 16-byte boundary.
         const bool ealign = aligned(e.u, 16) && aligned(e.r1, 16) && aligned(e.r2, 16);
         Launch l = base;
-        if (!strncmp(l.name, "mx_pw_", 6) && !(ealign && aligned(dev(sp.out), 16)))
+        if (!strncmp(l.name, "mx_pw_", 6) && !(ealign && aligned(dev(out), 16)))
             l = alt[g][0];  // the streaming kernels store 128 bits at a time
-        if (!strncmp(l.name, "mx_c3_", 6) && !aligned(dev(sp.out), 16)) l = alt[g][0];  // so does mx_c3
+        if (!strncmp(l.name, "mx_c3_", 6) && !aligned(dev(out), 16)) l = alt[g][0];  // so does mx_c3
         l.name = intern(std::string(l.name) + "_f");
         l.f = fn(l.name);
         if (l.kind == 1) {
             GemmArgs a;
             memcpy(&a, l.a0, sizeof a);
-            a.C = dev(sp.out);
+            a.C = dev(out);
             a.e = e;
             a.cvec = a.N % 4 == 0 && a.sC % 4 == 0 && aligned(a.C, 16) && ealign;
             set_args(l, a);
         } else if (l.kind == 2) {
             ConvArgs a;
             memcpy(&a, l.a0, sizeof a);
-            a.y = dev(sp.out);
+            a.y = dev(out);
             a.e = e;
             a.cvec = a.ow % 4 == 0 && aligned(a.y, 16) && ealign;
             set_args(l, a);
@@ -1419,6 +1450,37 @@ void Gpu::build_program(const mx_plan_desc *p) {
             throw Error("internal: a fused step whose producer has no epilogue");
         }
         return l;
+    };
+    // The launches of producer g: its epilogue, and a folded BlockPerm through
+    // the streaming kernels' block map - or, where they cannot take it
+    // (shape, alignment), the producer writing the permutation's source and
+    // the permutation's own launch after it.
+    auto gemm_part = [&](const StepSpec &sp, uint64_t g) -> std::vector<Launch> {
+        const Launch &base = ops[g][0];
+        if (sp.perm < 0) {
+            if (sp.epi) return {with_epilogue(sp, g, base, sp.out)};
+            return ops[g];
+        }
+        const mx_op &q = p->ops[sp.perm];
+        Launch l = base;
+        if (sp.epi) {
+            l = with_epilogue(sp, g, base, sp.out);
+        } else if (l.kind == 1) {
+            GemmArgs a;
+            memcpy(&a, l.a0, sizeof a);
+            a.C = dev(sp.out);
+            set_args(l, a);
+        }
+        if (!strncmp(l.name, "mx_pw_", 6) && aligned(dev(sp.out), 16)) {
+            GemmArgs a;
+            memcpy(&a, l.a0, sizeof a);
+            a.ymap = BlockMap{q.h * q.wd, 1, (int32_t)q.p[2], (int32_t)q.p[3], (int32_t)q.p[1], (int32_t)q.wd, 0};
+            set_args(l, a);
+            return {l};
+        }
+        std::vector<Launch> v{sp.epi ? with_epilogue(sp, g, base, sp.pout) : base};
+        for (const Launch &x : ops[sp.perm]) v.push_back(x);
+        return v;
     };
     prog.clear();
     for (const StepSpec &sp : pg.specs) {
@@ -1451,7 +1513,7 @@ void Gpu::build_program(const mx_plan_desc *p) {
         }
         if (sp.ln < 0) {
             if (sp.out < 0) prog.push_back(Step{sp.first, sp.last, ops[sp.first]});
-            else prog.push_back(Step{sp.first, sp.last, {with_epilogue(sp, sp.first, ops[sp.first][0])}});
+            else prog.push_back(Step{sp.first, sp.last, gemm_part(sp, sp.first)});
             continue;
         }
         // A LayerNorm folded into the next op's streaming GEMM: the
@@ -1463,12 +1525,13 @@ void Gpu::build_program(const mx_plan_desc *p) {
         memcpy(&la, ops[sp.first][0].a0, sizeof la);
         float *stats = scratch + ln_off;
         const bool ok = !strncmp(conv.name, "mx_pw_ch", 8) && aligned(la.x, 16) && la.hw % 4 == 0;
-        Launch gl = sp.out < 0 ? conv : with_epilogue(sp, g, conv);
+        std::vector<Launch> gp = gemm_part(sp, g);
+        Launch &gl = gp[0];
         if (!ok || strncmp(gl.name, "mx_pw_ch", 8)) {
             // not streaming (shape or alignment): the LayerNorm runs on its own
             Step st{sp.first, sp.last, ops[sp.first]};
-            st.launches.push_back(gl);
-            st.main = st.launches.size() - 1;
+            st.main = st.launches.size();
+            for (const Launch &x : gp) st.launches.push_back(x);
             prog.push_back(st);
             continue;
         }
@@ -1494,7 +1557,8 @@ void Gpu::build_program(const mx_plan_desc *p) {
         a.B = la.x;
         a.ln = LnIn{stats, stats + ln.hw, la.scale, la.bias};
         set_args(gl, a);
-        Step st{sp.first, sp.last, {sl, gl}};
+        Step st{sp.first, sp.last, {sl}};
+        for (const Launch &x : gp) st.launches.push_back(x);
         st.main = 1;
         prog.push_back(st);
     }

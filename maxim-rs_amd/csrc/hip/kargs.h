@@ -116,6 +116,17 @@ struct LnIn {
     const float *mean, *rstd, *scale, *bias;
 };
 
+// A block permutation folded into a GEMM's stores (BlockPerm backward, no
+// swap, src/model.rs:104-106): output element e (counted from C) is written
+// at (e / plane) * plane + map(e % plane), where map takes the blocked index
+// g * fh * fw + fy * fw + fx (g = gy * gw + gx) to the image index
+// (gy * fh + fy) * wd + gx * fw + fx. fw % 4 == 0 keeps four consecutive
+// outputs contiguous.
+struct BlockMap {
+    int64_t plane;
+    int32_t on, fh, fw, gw, wd, pad;
+};
+
 struct GemmArgs {
     const float *A;
     const float *B;
@@ -128,6 +139,7 @@ struct GemmArgs {
     int32_t cvec, pad;    // 1: C, u, r1, r2 are 16-byte aligned (128-bit stores)
     Epilogue e;
     LnIn ln;
+    BlockMap ymap;
 };
 
 // Small GEMV for the plane-1 CALayer convs: y[o] = b[o] + sum_i w[o][i] x[i].

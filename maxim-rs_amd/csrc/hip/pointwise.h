@@ -269,7 +269,18 @@ __device__ void body(const GemmArgs &a) {
                 v[3] = v[3] + o2[bi].w;
             }
         }
-        st4(Y + off, make_float4(v[0], v[1], v[2], v[3]));
+        int64_t at = off;
+        if (a.ymap.on) {  // a folded block permutation: the image position
+            // (32-bit: the host enables the map only below 2^31 elements)
+            const BlockMap &q = a.ymap;
+            const uint32_t e = (uint32_t)(b * a.sC + off), pl = (uint32_t)q.plane;
+            const uint32_t base = e / pl * pl, idx = e - base, pp = (uint32_t)(q.fh * q.fw);
+            const uint32_t gi = idx / pp, p = idx - gi * pp;
+            const uint32_t gy = gi / (uint32_t)q.gw, gx = gi - gy * (uint32_t)q.gw;
+            const uint32_t fy = p / (uint32_t)q.fw, fx = p - fy * (uint32_t)q.fw;
+            at = (int64_t)(base + (gy * q.fh + fy) * q.wd + gx * q.fw + fx) - b * a.sC;
+        }
+        st4(Y + at, make_float4(v[0], v[1], v[2], v[3]));
     }
 }
 

@@ -188,3 +188,53 @@ def test_layernorm_folded_into_the_dense(gpu_ok, c, co, h, w, act):
     else:
         assert [(a, b) for a, b, _ in steps] == [(0, 1), (1, 2)], steps
     check(got, oracle_plan(cp, {0: x}, out), "ln %d -> conv1x1 %d->%d @%dx%d%s" % (c, c, co, h, w, " + gelu" if act else ""))
+
+
+def perm_case(kind, fw, misalign=False):
+    """A producer whose output a backward BlockPerm (src/model.rs:104-106)
+    scatters to the image: conv1x1 + residual add, or GateMm mode 0 / 1 over
+    the blocked tensor. Buffers: X, R, T, S, pad, Y (the image)."""
+    from maxim_amd import plan as P
+    gh, gw, fh = 4, 4, 8  # 16 cells: GateMm mode 0 reduces over 16
+    h, w = gh * fh, gw * fw
+    G, Pp = gh * gw, fh * fw
+    rng = np.random.default_rng(fw + len(kind) + misalign)
+    c = 16 if kind != "conv" else 32
+    bl = (c, G, Pp)
+    bufs = [bl, bl, bl, bl, (1, 1, 1 if misalign else 4), (c, h, w)]
+    X, R, T, S, Y = 0, 1, 2, 3, 5
+    inputs = {X: rng.standard_normal(bl).astype(np.float32), R: rng.standard_normal(bl).astype(np.float32)}
+    perm = P.make_op(P.BLOCK_PERM, dst=Y, src=S, c=c, h=h, wd=w, mode=0, p=[gh, gw, fh, fw])
+    if kind == "conv":
+        wt = he(rng, (c, c), c)
+        b = (rng.standard_normal(c) * 0.1).astype(np.float32)
+        ops = [P.make_op(P.CONV1X1, dst=T, src=X, w=0, bias=1, c_in=c, c_out=c, h=G, wd=Pp),
+               P.make_op(P.ADD, dst=S, src=T, src2=R, n=c * G * Pp), perm]
+    else:
+        mode = 0 if kind == "gate0" else 1
+        k = G if mode == 0 else Pp
+        wt = he(rng, (k, k), k)
+        b = (rng.standard_normal(k) * 0.1).astype(np.float32)
+        ops = [P.make_op(P.GATE_MM, dst=S, src=X, w=0, bias=1, c=c, mode=mode, p=[G, Pp]), perm]
+    cp = P.CustomPlan(bufs, ops, [wt, b], input=X, output=Y, align=1)
+    return cp, inputs, Y
+
+
+@pytest.mark.parametrize("kind,fw,misalign", [
+    ("conv", 8, False), ("gate0", 8, False), ("gate1", 8, False),   # folded into the stores
+    ("conv", 12, False), ("gate1", 16, False),
+    ("conv", 6, False), ("gate0", 10, False),                       # cells not a multiple of 4 wide
+    ("conv", 8, True), ("gate0", 8, True),                          # image one float off 16 bytes
+])
+def test_block_permutation_folded_into_the_stores(gpu_ok, kind, fw, misalign):
+    cp, inputs, Y = perm_case(kind, fw, misalign)
+    assert (int(cp.offs[Y]) % 4 != 0) == misalign
+    got, steps = run_plan(cp, inputs, Y)
+    print("steps", steps)
+    n = len(cp.ops)
+    if fw % 4 == 0:
+        assert len(steps) == 1 and (steps[0][0], steps[0][1]) == (0, n), steps
+        assert steps[0][2].startswith("mx_pw_") or misalign
+    else:
+        assert steps[-1][:2] == (n - 1, n) and steps[-1][2].startswith("mx_block_perm"), steps
+    check(got, oracle_plan(cp, inputs, Y), "%s -> block_perm, fw %d, misaligned %d" % (kind, fw, misalign))
