@@ -39,6 +39,7 @@ struct Launch {
     const char *name = "";
     unsigned g[3] = {1, 1, 1};
     unsigned b[3] = {MXK_BLOCK, 1, 1};
+    unsigned shm = 0;  // dynamic LDS bytes
     alignas(16) unsigned char a0[192];
     alignas(16) unsigned char a1[32];
     int nparams = 1;
@@ -130,6 +131,26 @@ struct ResizeTab {
     const float *t;
     int32_t maxt, pad;
 };
+
+// The one-pass resize stages, per block of `rows` output rows, the input rows
+// from the first row's first vertical tap to the last row's last one. Returns
+// the most any block needs, or -1 if some row of a block reaches outside that
+// range (taps not monotone), in which case the two-pass kernels run.
+constexpr int kResizeRowsMax = 96, kResizeTapsMax = 8;
+int resize_band(const std::vector<float> &tv, int mt, int64_t n_out, int64_t rows) {
+    const size_t sv = 3 + (size_t)mt;
+    int most = 0;
+    for (int64_t o0 = 0; o0 < n_out; o0 += rows) {
+        const int64_t o1 = std::min(o0 + rows, n_out);
+        const int lo = (int)tv[o0 * sv], hi = (int)tv[(o1 - 1) * sv] + (int)tv[(o1 - 1) * sv + 1];
+        for (int64_t o = o0; o < o1; ++o) {
+            const int j0 = (int)tv[o * sv], n = (int)tv[o * sv + 1];
+            if (j0 < lo || j0 + n > hi) return -1;
+        }
+        most = std::max(most, hi - lo);
+    }
+    return most;
+}
 
 // The GEMM tile for an M x N problem (times `batch`): estimated time is the
 // number of rounds of resident blocks (two per CU) times the tile's cost,
@@ -303,7 +324,7 @@ public:
     }
     void launch(Launch &l) {
         void *params[2] = {l.a0, l.a1};
-        check(H.hipModuleLaunchKernel(l.f, l.g[0], l.g[1], l.g[2], l.b[0], l.b[1], l.b[2], 0, stream,
+        check(H.hipModuleLaunchKernel(l.f, l.g[0], l.g[1], l.g[2], l.b[0], l.b[1], l.b[2], l.shm, stream,
                                       params, nullptr),
               l.name);
         ++kernels;
@@ -358,7 +379,7 @@ public:
             void *params[2] = {l.a0, l.a1};
             const uint64_t gx = (uint64_t)l.g[0] * l.b[0], gy = (uint64_t)l.g[1] * l.b[1], gz = (uint64_t)l.g[2] * l.b[2];
             if (gx > 0xffffffffULL || gy > 0xffffffffULL || gz > 0xffffffffULL) throw Error("a timed launch exceeds 2^32 work-items");
-            check(H.hipExtModuleLaunchKernel(l.f, (uint32_t)gx, (uint32_t)gy, (uint32_t)gz, l.b[0], l.b[1], l.b[2], 0,
+            check(H.hipExtModuleLaunchKernel(l.f, (uint32_t)gx, (uint32_t)gy, (uint32_t)gz, l.b[0], l.b[1], l.b[2], l.shm,
                                              stream, params, nullptr, ev[2 * k], ev[2 * k + 1], 0),
                   l.name);
             ++kernels;
@@ -1006,6 +1027,36 @@ void Gpu::build_launches(const mx_plan_desc *p, const std::vector<int64_t> &woff
                 break;
             }
             case MX_OP_RESIZE: {
+                // One pass when the taps of both axes are at most 8 and a
+                // band of output rows reads few enough input rows: the most
+                // rows per block that still leaves >= 2048 blocks, else the
+                // band with the most blocks.
+                if (maxt[i][0] <= kResizeTapsMax && !std::getenv("MAXIM_RESIZE_2PASS")) {
+                    int mv = 0;
+                    const std::vector<float> tv = resize_table(o.h, o.oh, mv);
+                    const int64_t tiles_x = cdiv(o.ow, 64);
+                    int64_t pick = 0;
+                    int pick_band = 0;
+                    for (int64_t rows : {64, 32, 16, 8, 4, 2, 1}) {
+                        const int band = resize_band(tv, mv, o.oh, rows);
+                        if (band < 0 || band > kResizeRowsMax) continue;
+                        pick = rows;
+                        pick_band = band;
+                        if (tiles_x * cdiv(o.oh, rows) * o.c >= 2048) break;
+                    }
+                    if (pick > 0 && mv <= kResizeTapsMax) {
+                        Resize2Args r{B(o.src), B(o.dst), X(i, 0), X(i, 1), (int32_t)o.h, (int32_t)o.wd,
+                                      (int32_t)o.oh, (int32_t)o.ow, maxt[i][0], maxt[i][1], (int32_t)pick,
+                                      (int32_t)tiles_x, pick_band, 0};
+                        Launch l = mk("mx_resize_hv");
+                        l.g[0] = (uint32_t)(tiles_x * cdiv(o.oh, pick));
+                        l.g[1] = (uint32_t)o.c;
+                        l.shm = (unsigned)(4 * (pick_band * 64 + pick * (3 + mv)));
+                        set_args(l, r);
+                        L.push_back(l);
+                        break;
+                    }
+                }
                 ResizeArgs h{};
                 h.x = B(o.src);
                 h.y = B(o.src2);

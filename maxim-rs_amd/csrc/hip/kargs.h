@@ -82,6 +82,18 @@ struct ResizeArgs {
     int32_t n_in, n_out, width, axis;
 };
 
+// Both resize axes in one pass (mx_resize_hv): tap tables as for the
+// two-pass kernels, `rows` output rows x 64 output columns per block.
+struct Resize2Args {
+    const float *x;
+    float *y;
+    const float *th, *tv;   // tap tables: horizontal (per output column), vertical (per output row)
+    int32_t h, wd, oh, ow;  // input and output plane
+    int32_t mth, mtv;       // taps per table row
+    int32_t rows, tiles_x;  // output rows per block, column tiles per row band
+    int32_t band, pad;      // LDS rows of horizontal results (the most any block needs)
+};
+
 // Nearest subsample.
 struct DownArgs {
     const float *x;

@@ -435,3 +435,73 @@ extern "C" __global__ __launch_bounds__(MXK_BLOCK) void mx_resize_v(ResizeArgs a
     for (int k = 0; k < nt; ++k) acc += e[3 + k] * src[(int64_t)k * a.width];
     a.y[i] = ws > 0.0f ? acc / ws : acc;
 }
+
+// Both axes in one pass, without the intermediate plane. A block owns 64
+// output columns x `rows` output rows of one channel: it first runs the
+// horizontal pass for the input rows those outputs read (the vertical taps of
+// its first row through those of its last, at most `band` rows, which the host
+// sizes the dynamic LDS for) into LDS, with the band's vertical taps beside
+// them, then the vertical pass from LDS to the output. Every intermediate value
+// is computed by the same expression as in mx_resize_h, so the result is
+// bit-identical to the two-pass kernels; rows shared by two blocks are simply
+// computed twice. Both tables are at most RS_MAXT taps wide (checked by the
+// host); the horizontal taps of a lane's column live in registers.
+constexpr int RS_TW = 64;
+constexpr int RS_MAXT = 8;
+
+extern "C" __global__ __launch_bounds__(256) void mx_resize_hv(Resize2Args a) {
+    extern __shared__ float rs_lds[];
+    float *tmp = rs_lds;                     // [band][64]
+    float *vt = rs_lds + a.band * RS_TW;     // [rows][3 + mtv]
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int ch = blockIdx.y;
+    const int tx = blockIdx.x % a.tiles_x, ty = blockIdx.x / a.tiles_x;
+    const int ox0 = tx * RS_TW, oy0 = ty * a.rows;
+    const int nrow = min(a.rows, a.oh - oy0);
+    const int sv = 3 + a.mtv, sh = 3 + a.mth;
+    const float *vf = a.tv + (int64_t)oy0 * sv, *vl = vf + (int64_t)(nrow - 1) * sv;
+    const int jlo = (int)vf[0];
+    const int nr = (int)vl[0] + (int)vl[1] - jlo;
+    for (int q = threadIdx.x; q < nrow * sv; q += 256) vt[q] = vf[q];
+
+    const int ox = ox0 + lane;
+    const bool col = ox < a.ow;
+    int j0 = 0, nt = 0;
+    float ws = 0.0f, w[RS_MAXT];
+    if (col) {
+        const float *e = a.th + (int64_t)ox * sh;
+        j0 = (int)e[0];
+        nt = (int)e[1];
+        ws = e[2];
+    }
+#pragma unroll
+    for (int k = 0; k < RS_MAXT; ++k) w[k] = (col && k < a.mth) ? a.th[(int64_t)ox * sh + 3 + k] : 0.0f;
+    const float *xs = a.x + (int64_t)ch * a.h * a.wd + j0 + (int64_t)jlo * a.wd;
+    if (col) {
+#pragma unroll 2
+        for (int r = wave; r < nr; r += 4) {
+            const float *s = xs + (int64_t)r * a.wd;
+            float acc = 0.0f;
+#pragma unroll
+            for (int k = 0; k < RS_MAXT; ++k)
+                if (k < nt) acc += w[k] * s[k];
+            tmp[r * RS_TW + lane] = ws > 0.0f ? acc / ws : acc;
+        }
+    }
+    __syncthreads();
+    if (!col) return;
+    float *yc = a.y + ((int64_t)ch * a.oh + oy0) * a.ow + ox;
+#pragma unroll 2
+    for (int r = wave; r < nrow; r += 4) {
+        const float *e = vt + r * sv;
+        const int b = (int)e[0] - jlo, n = (int)e[1];
+        const float vs = e[2];
+        const float *t = tmp + b * RS_TW + lane;
+        float acc = 0.0f;
+#pragma unroll
+        for (int k = 0; k < RS_MAXT; ++k)
+            if (k < n) acc += e[3 + k] * t[k * RS_TW];
+        yc[(int64_t)r * a.ow] = vs > 0.0f ? acc / vs : acc;
+    }
+}
