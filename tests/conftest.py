@@ -70,3 +70,60 @@ def gpu_ok():
     if not H.driver_ready():
         pytest.fail("no HIP device: the gpu tests need an MI355X")
     return True
+
+
+# Per-op bars of the lockstep walks (the reference's --verify-gpu uses
+# max|d| <= 1e-3 * max|cpu| for every op, src/main.rs:709-712):
+#   exact     ops whose arithmetic the executor reproduces term for term
+#   ulps      gelu, sigmoid (device erff / expf vs libm): |d| <= 4e-7 * (1 + |x|)
+#   rounding  chan_mean and every matrix-core GEMM: max|d| <= 1e-4 * max|cpu|
+EXACT = {"copy", "add", "mul", "gate_apply", "lrelu", "chan_scale", "chan_ln", "block_perm",
+         "down_s", "resize"}
+ULPS = {"gelu", "sigmoid"}
+
+
+def op_sources(plan, op):
+    """The arena buffers an op reads (a resize's second operand is its scratch)."""
+    from maxim_amd import plan as P
+    return [op.src] if op.kind == P.RESIZE else plan.operands(op)[1:]
+
+
+def _max_abs_diff(got, want, x=None, chunk=1 << 25):
+    """max |got - want| (divided by 1 + |x| where x is given) in float64, in
+    chunks, so that billion-element buffers need no billion-element
+    temporaries."""
+    m = 0.0
+    for a in range(0, want.size, chunk):
+        d = np.abs(got[a:a + chunk].astype(np.float64) - want[a:a + chunk])
+        if x is not None:
+            d /= 1.0 + np.abs(x[a:a + chunk].astype(np.float64))
+        if d.size:
+            m = max(m, float(d.max()))
+    return m
+
+
+def judge_op(plan, arena, op, got):
+    """(ok, kind key, error) of the device result `got` for `op` against the
+    oracle's result already in `arena`."""
+    from maxim_amd import plan as P
+    name = P.OP_NAMES[op.kind]
+    want = buf(plan, arena, op.dst)
+    if op.kind in (P.COPY, P.GELU, P.LRELU, P.SIGMOID):
+        want = want[:op.n]
+    got = got[:want.size]
+    exact = name in EXACT or (op.kind == P.CONV1X1 and op.h * op.wd == 1)
+    if exact:
+        ok = np.array_equal(got.view(np.uint32), want.view(np.uint32))
+        if not ok:
+            ok = np.array_equal(got, want) and not np.isnan(want).any()
+        rel = 0.0 if ok else _max_abs_diff(got, want)
+    elif name in ULPS:
+        rel = _max_abs_diff(got, want, buf(plan, arena, op.src)[:op.n])
+        ok = rel <= 4e-7
+    else:
+        scale = float(np.abs(want).max()) if want.size else 0.0
+        rel = _max_abs_diff(got, want)
+        rel = rel / scale if scale > 0 else rel
+        ok = rel <= 1e-4
+    key = "gemv" if exact and op.kind == P.CONV1X1 else name
+    return ok, key, rel

@@ -18,17 +18,12 @@ BIT-EXACT:
 import numpy as np
 import pytest
 
-from conftest import buf, smooth_image, weights
+from conftest import EXACT, buf, judge_op, op_sources, smooth_image, weights
 
 pytestmark = pytest.mark.gpu
 
-EXACT = {"copy", "add", "mul", "gate_apply", "lrelu", "chan_scale", "chan_ln", "block_perm",
-         "down_s", "resize"}
-ULPS = {"gelu", "sigmoid"}
-
 
 def walk(plan, img, report):
-    from maxim_amd import plan as P
     from maxim_amd import hip as H
     from oracle import oracle as O
 
@@ -40,36 +35,14 @@ def walk(plan, img, report):
     worst = {}
     failures = []
     for i, op in enumerate(plan.ops):
-        name = P.OP_NAMES[op.kind]
-        srcs = plan.operands(op)[1:]
-        if op.kind == P.RESIZE:
-            srcs = [op.src]
-        for s in srcs:
+        for s in op_sources(plan, op):
             gpu.write_buf(s, buf(plan, arena, s))
         gpu.step_op(i)
         O.step(plan, arena, i)
-        want = buf(plan, arena, op.dst)
-        if op.kind in (P.COPY, P.GELU, P.LRELU, P.SIGMOID):
-            want = want[:op.n]
-        got = gpu.read_buf(op.dst)[:want.size]
-        d = np.abs(got.astype(np.float64) - want)
-        scale = float(np.abs(want).max()) if want.size else 0.0
-        exact = name in EXACT or (op.kind == P.CONV1X1 and op.h * op.wd == 1)
-        if exact:
-            ok = np.array_equal(got.view(np.uint32), want.view(np.uint32)) or (
-                np.array_equal(got, want) and not np.isnan(want).any())
-            rel = float(d.max()) if d.size else 0.0
-        elif name in ULPS:
-            x = buf(plan, arena, op.src)[:op.n].astype(np.float64)
-            rel = float((d / (1.0 + np.abs(x))).max()) if d.size else 0.0
-            ok = rel <= 4e-7
-        else:
-            rel = float(d.max()) / scale if scale > 0 else float(d.max())
-            ok = rel <= 1e-4
-        key = name if not exact or op.kind != P.CONV1X1 else "gemv"
+        ok, key, rel = judge_op(plan, arena, op, gpu.read_buf(op.dst))
         worst[key] = max(worst.get(key, 0.0), rel)
         if not ok:
-            failures.append("op %d %s: %s %.3g" % (i, op.describe(), "differs" if exact else "err", rel))
+            failures.append("op %d %s: %s %.3g" % (i, op.describe(), "differs" if key in EXACT else "err", rel))
     report(worst)
     gpu.close()
     return failures
