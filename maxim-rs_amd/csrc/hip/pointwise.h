@@ -251,7 +251,7 @@ __device__ void body(const GemmArgs &a) {
             }
             if (a.e.act == MXK_ACT_GELU) {
 #pragma unroll
-                for (int u = 0; u < 4; ++u) v[u] = gelu_erf(v[u]);
+                for (int u = 0; u < 4; ++u) v[u] = gelu(v[u]);
             } else if (a.e.act == MXK_ACT_LRELU) {
 #pragma unroll
                 for (int u = 0; u < 4; ++u) v[u] = v[u] >= 0.0f ? v[u] : a.e.slope * v[u];

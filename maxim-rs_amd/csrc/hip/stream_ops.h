@@ -5,8 +5,9 @@
 // Arithmetic follows the reference's CPU arms term for term (src/exec_cpu.rs
 // 537-598, 377-434, 1075-1178) and this file is compiled without FP
 // contraction, so add / mul / gate / lrelu / chan_scale / chan_ln /
-// block_perm / down_s / resize reproduce the CPU path bit for bit; gelu and
-// sigmoid differ from it only through the device erff / expf.
+// block_perm / down_s / resize reproduce the CPU path bit for bit; sigmoid
+// differs from it only through the device expf, gelu through its erf
+// approximation (common.h, within 2.2e-7 * (1 + |x|) of the exact function).
 #pragma once
 
 #include "common.h"
@@ -19,7 +20,7 @@ __device__ __forceinline__ float ew1(float a, float b, float slope) {
     if (OP == MXK_ADD) return a + b;
     if (OP == MXK_MUL) return a * b;
     if (OP == MXK_GATE_APPLY) return a * (b + 1.0f);
-    if (OP == MXK_GELU) return gelu_erf(a);
+    if (OP == MXK_GELU) return gelu(a);
     if (OP == MXK_LRELU) return a >= 0.0f ? a : slope * a;
     return 1.0f / (1.0f + expf(-a));  // MXK_SIGMOID
 }
