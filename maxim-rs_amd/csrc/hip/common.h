@@ -14,6 +14,22 @@ __device__ __forceinline__ f32x4 mfma16(float a, float b, f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
 }
 
+// Work-group placement. The dispatcher deals consecutive work-group ids to
+// the 8 XCDs in turn, and each XCD has its own L2, so neighbouring tiles
+// (which share halo rows, cache lines and operands) land in different L2s.
+// xcd_tile() renumbers the (gridDim.x x gridDim.y) grid so that each XCD
+// walks one contiguous run of the new ids, and splits the new id into a tile
+// index and a band (e.g. the output-channel block) with the band fastest, so
+// every band of a tile is computed under the same L2.
+__device__ __forceinline__ void xcd_tile(int &tile, int &band) {
+    const int gy = gridDim.y, n = gridDim.x * gy;
+    const int id = blockIdx.x + blockIdx.y * gridDim.x;
+    const int x = id & 7, q = n >> 3, r = n & 7;
+    const int nid = x * q + min(x, r) + (id >> 3);
+    tile = nid / gy;
+    band = nid - tile * gy;
+}
+
 __device__ __forceinline__ float4 ld4(const float *p) { return *reinterpret_cast<const float4 *>(p); }
 __device__ __forceinline__ void st4(float *p, float4 v) { *reinterpret_cast<float4 *>(p) = v; }
 

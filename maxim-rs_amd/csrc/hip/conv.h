@@ -43,8 +43,10 @@ __device__ void body(const ConvArgs &a) {
     const int wm = wave / WAVES_N, wn = wave % WAVES_N;
     const int lr = lane & 15, lk = lane >> 4;
     const int tiles_x = (a.ow + TW - 1) / TW;
-    const int ty0 = (blockIdx.x / tiles_x) * TH, tx0 = (blockIdx.x % tiles_x) * TW;
-    const int mb = blockIdx.y, m0 = mb * BM;
+    int tile, mb;
+    xcd_tile(tile, mb);
+    const int ty0 = (tile / tiles_x) * TH, tx0 = (tile % tiles_x) * TW;
+    const int m0 = mb * BM;
     const int iy0 = ty0 * STRIDE - a.pad_top, ix0 = tx0 * STRIDE - a.pad_left;
     const int64_t plane = (int64_t)a.h * a.wd;
     const int nchunk = (a.ci + CK - 1) / CK;

@@ -53,8 +53,10 @@ __device__ void body(const ConvArgs &a) {
     const int wm = wave / WAVES_N, wn = wave % WAVES_N;
     const int i = lane & 15, g = lane >> 4;
     const int tiles_x = (a.wd + 15) / 16;
-    const int ty0 = (blockIdx.x / tiles_x) * TH, tx0 = (blockIdx.x % tiles_x) * 16;
-    const int mb = blockIdx.y, m0 = mb * BM;
+    int tile, mb;
+    xcd_tile(tile, mb);
+    const int ty0 = (tile / tiles_x) * TH, tx0 = (tile % tiles_x) * 16;
+    const int m0 = mb * BM;
     const int64_t plane = (int64_t)a.h * a.wd;
     const int nchunk = a.ci / CK;
     const float *wblk = a.w + (int64_t)mb * nchunk * (BM * 9 * CK);
