@@ -11,7 +11,8 @@ in HBM when the timed region starts. Prints ONE JSON line:
                 MFMA 157.3 TFLOP/s or HBM 8 TB/s): algorithmic FLOPs or bytes
                 per launch over the average launch duration, from the HIP
                 start/stop events each dispatch records on the executor's
-                stream over K further (eager) passes
+                stream over K further (eager) passes; `traffic` = its measured
+                HBM-side bytes per launch (profiles/hbm_traffic_c4.md)
   cpu_baseline  the CPU path (oracle/, a C restatement of the reference's
                 src/exec_cpu.rs) timed on this host over one full pass
 
@@ -143,7 +144,7 @@ def main():
     else:
         roof = {"bound": "hbm", "achieved": by / nl / avg_s / 1e9, "peak": 8000.0, "unit": "GB/s"}
     roof["frac"] = roof["achieved"] / roof["peak"]
-    roof["traffic"] = None
+    roof["traffic"] = traffic_per_launch(kern)
     roof["kernel"] = kern
     roof["avg_launch_us"] = avg_s * 1e6
     roof["launches_per_step"] = nl // args.steps
@@ -193,6 +194,25 @@ def main():
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)
+
+
+TRAFFIC = os.path.join(ROOT, "profiles", "hbm_traffic_c4.md")
+
+
+def traffic_per_launch(kernel):
+    """HBM-side bytes per launch of `kernel` at C4, from the committed
+    rocprofv3 summary (FETCH_SIZE and WRITE_SIZE passes, each scaled by what
+    the counter reads for a copy of known size); None if the kernel is not in
+    it."""
+    try:
+        rows = open(TRAFFIC).read().splitlines()
+    except OSError:
+        return None
+    for r in rows:
+        cells = [c.strip() for c in r.strip().strip("|").split("|")]
+        if len(cells) == 5 and cells[0] == kernel:
+            return float(cells[4]) * 1e6
+    return None
 
 
 def launch_costs(plan, steps, launches, R):

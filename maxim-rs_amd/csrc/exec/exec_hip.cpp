@@ -40,7 +40,7 @@ struct Launch {
     unsigned g[3] = {1, 1, 1};
     unsigned b[3] = {MXK_BLOCK, 1, 1};
     unsigned shm = 0;  // dynamic LDS bytes
-    alignas(16) unsigned char a0[192];
+    alignas(16) unsigned char a0[256];
     alignas(16) unsigned char a1[32];
     int nparams = 1;
     int kind = 0;  // 1: a0 holds GemmArgs (plain epilogue), 2: ConvArgs
@@ -239,7 +239,7 @@ std::string conv_name(ConvCfg c, bool k3) {
 
 // What the executor decides about a plan before touching the device: which
 // ops fuse into which steps, and where every buffer lives in the device arena.
-enum { RULE_NONE = 0, RULE_CA_MLP = 1, RULE_SCALE_ADD = 2, RULE_ELIDED = 3 };
+enum { RULE_NONE = 0, RULE_CA_MLP = 1, RULE_SCALE_ADD = 2, RULE_ELIDED = 3, RULE_PERM_IN = 4 };
 
 struct StepSpec {
     uint64_t first = 0, last = 0;
@@ -250,6 +250,11 @@ struct StepSpec {
     int64_t out = -1, u = -1, r1 = -1, r2 = -1;
     int act = MXK_ACT_NONE;
     float slope = 0.0f;
+    // An elided forward BlockPerm (op xperm / rperm, RULE_PERM_IN): the folded
+    // LayerNorm's GEMM reads its source xsrc through the block map, and the
+    // residual step reads r1 (then the source) at its stores' image positions
+    // (r1p: the permutation's output, read instead if a kernel cannot map).
+    int64_t xperm = -1, xsrc = -1, rperm = -1, r1p = -1;
 };
 
 struct Program {
@@ -1366,6 +1371,99 @@ void Program::plan_fusion(const mx_plan_desc *p, bool require_clear) {
         specs.push_back(sp);
         i = sp.last;
     }
+
+    // Forward BlockPerm elision. The gMLP branches permute x into blocked
+    // order P, LayerNorm P straight into a 1x1 conv (folded above), and later
+    // add P back as the residual of an out-projection whose stores are folded
+    // into the backward permutation of the same geometry into x itself. LN
+    // is per pixel, so both readers can take x in image order through the
+    // block map instead: the folded LayerNorm's GEMM reads its columns (and
+    // the statistics) at the mapped positions, and the residual is read at
+    // the position the output is stored to. The permutation then launches
+    // nothing. Requires: P read by exactly those two ops, x unwritten until
+    // the backward permutation writes it back (each element then read and
+    // rewritten by one thread), whole buffers, fw % 4 == 0, < 2^31 elements.
+    auto readers_after = [&](int64_t x, uint64_t i) {
+        std::vector<uint64_t> who;
+        std::vector<R> live{range(x)};
+        for (uint64_t k = i + 1; k < p->n_ops && !live.empty(); ++k) {
+            const mx_op &o = p->ops[k];
+            bool reads = false;
+            for (int64_t s : reads_of(o))
+                for (const R &l : live) reads = reads || overlap(range(s), l);
+            if (reads) who.push_back(k);
+            for (int64_t d : writes_of(o)) {
+                const R w = range(d);
+                std::vector<R> rest;
+                for (const R &l : live) {
+                    if (!overlap(w, l)) { rest.push_back(l); continue; }
+                    if (l.a < w.a) rest.push_back(R{l.a, w.a});
+                    if (w.b < l.b) rest.push_back(R{w.b, l.b});
+                }
+                live.swap(rest);
+            }
+        }
+        return who;
+    };
+    std::vector<int64_t> spec_of(p->n_ops, -1);
+    for (uint64_t s = 0; s < specs.size(); ++s)
+        for (uint64_t k = specs[s].first; k < specs[s].last; ++k) spec_of[k] = (int64_t)s;
+    for (uint64_t j = 0; j + 2 < p->n_ops; ++j) {
+        const mx_op &q = p->ops[j];
+        if (q.kind != MX_OP_BLOCK_PERM || !(q.mode & MX_PERM_FORWARD) || (q.mode & MX_PERM_SWAP)) continue;
+        const int64_t P = q.dst, S = q.src;
+        const uint64_t n = (uint64_t)(q.c * q.h * q.wd);
+        if (q.p[0] * q.p[2] != q.h || q.p[1] * q.p[3] != q.wd || q.p[3] % 4 || q.wd % 4 || n >= (1ULL << 31)) continue;
+        if (range(P).b - range(P).a != n || range(S).b - range(S).a != n || overlap(range(P), range(S))) continue;
+        if ((uint64_t)P == p->output || (p->keep && p->keep[P])) continue;
+        StepSpec &J = specs[spec_of[j]];
+        if (J.first != j || J.last != j + 1 || J.rule != RULE_NONE) continue;
+        // A GateMm straight on P (the cross-gating blocks): its X is P's
+        // [cells][pixels] per channel, read from S through the token map.
+        const mx_op &gm = p->ops[j + 1];
+        if (gm.kind == MX_OP_GATE_MM && gm.src == P) {
+            StepSpec &G = specs[spec_of[j + 1]];
+            const bool adv = gm.mode == 0 ? 16 % q.p[1] == 0 : 16 % q.p[3] == 0;  // 16 k's = whole rows
+            if (G.first != j + 1 || G.rule != RULE_NONE || G.ln >= 0 || !adv || gm.c != q.c ||
+                gm.p[0] != q.p[0] * q.p[1] || gm.p[1] != q.p[2] * q.p[3])
+                continue;
+            const std::vector<uint64_t> who = readers_after(P, j);
+            if (who.size() != 1 || who[0] != j + 1 || !clear_of(G.out >= 0 ? G.out : gm.dst, {S})) continue;
+            J.rule = RULE_PERM_IN;
+            G.xperm = (int64_t)j;
+            G.xsrc = S;
+            ++fused_ops;
+            continue;
+        }
+        StepSpec &L = specs[spec_of[j + 1]];
+        if (L.ln != (int64_t)(j + 1) || p->ops[j + 1].src != P) continue;
+        int64_t sk = -1;
+        for (uint64_t s = spec_of[j + 1] + 1; s < specs.size() && sk < 0; ++s)
+            if (specs[s].r1 == P) sk = (int64_t)s;
+        if (sk < 0) continue;
+        StepSpec &K = specs[sk];
+        if (!K.epi || K.perm < 0 || K.u == P || K.r2 == P) continue;
+        const mx_op &bq = p->ops[K.perm];
+        if (bq.dst != S || bq.c != q.c || bq.h != q.h || bq.wd != q.wd || bq.p[0] != q.p[0] || bq.p[1] != q.p[1] ||
+            bq.p[2] != q.p[2] || bq.p[3] != q.p[3])
+            continue;
+        uint64_t add = 0;
+        for (uint64_t k = K.first; k < K.last; ++k)
+            if (p->ops[k].kind == MX_OP_ADD && (p->ops[k].src == P || p->ops[k].src2 == P)) add = k;
+        const std::vector<uint64_t> who = readers_after(P, j);
+        if (add == 0 || who.size() != 2 || who[0] != j + 1 || who[1] != add) continue;
+        bool ok = clear_of(L.out >= 0 ? L.out : p->ops[j + 2].dst, {S});
+        for (uint64_t k = j + 1; k < (uint64_t)K.perm && ok; ++k)
+            for (int64_t d : writes_of(p->ops[k])) ok = ok && !overlap(range(d), range(S));
+        if (!ok) continue;
+        J.rule = RULE_PERM_IN;
+        L.xperm = (int64_t)j;
+        L.xsrc = S;
+        K.rperm = (int64_t)j;
+        K.r1p = P;
+        K.r1 = S;
+        ++fused_ops;
+    }
 }
 
 // The device arena: the plan's own packing rule (largest first, first use as
@@ -1409,16 +1507,21 @@ void Program::layout(const mx_plan_desc *p, bool repack) {
     for (uint64_t i = 0; i < n; ++i) dbase[i] = base[i];
     const uint64_t DEAD = UINT64_MAX;
     std::vector<uint64_t> first(n, DEAD), last(n, 0);
-    for (uint64_t s = 0; s < specs.size(); ++s)
+    for (uint64_t s = 0; s < specs.size(); ++s) {
+        auto use = [&](int64_t b) {
+            if (b < 0) return;
+            const int64_t r = base[b];
+            if (first[r] == DEAD) first[r] = s;
+            last[r] = std::max(last[r], s);
+        };
         for (uint64_t k = specs[s].first; k < specs[s].last; ++k) {
             const mx_op &o = p->ops[k];
-            for (int64_t b : {o.dst, o.src, o.src2}) {
-                if (b < 0) continue;
-                const int64_t r = base[b];
-                if (first[r] == DEAD) first[r] = s;
-                last[r] = std::max(last[r], s);
-            }
+            for (int64_t b : {o.dst, o.src, o.src2}) use(b);
         }
+        // buffers a step reads in place of an elided permutation's output
+        use(specs[s].xsrc);
+        use(specs[s].r1);
+    }
     if (p->keep)
         for (uint64_t i = 0; i < n; ++i)
             if (p->keep[i] && first[base[i]] != DEAD) last[base[i]] = specs.size() - 1;
@@ -1506,6 +1609,12 @@ void Gpu::build_program(const mx_plan_desc *p) {
     // the streaming kernels' block map - or, where they cannot take it
     // (shape, alignment), the producer writing the permutation's source and
     // the permutation's own launch after it.
+    // An elided forward permutation's step, by op, and what restores it
+    // when a reader cannot take the block map after all.
+    std::vector<int64_t> perm_step(p->n_ops, -1);
+    auto restore_perm = [&](int64_t j) {
+        if (j >= 0 && perm_step[j] >= 0) prog[perm_step[j]].launches = ops[j];
+    };
     auto gemm_part = [&](const StepSpec &sp, uint64_t g) -> std::vector<Launch> {
         const Launch &base = ops[g][0];
         if (sp.perm < 0) {
@@ -1525,17 +1634,49 @@ void Gpu::build_program(const mx_plan_desc *p) {
         if (!strncmp(l.name, "mx_pw_", 6) && aligned(dev(sp.out), 16)) {
             GemmArgs a;
             memcpy(&a, l.a0, sizeof a);
-            a.ymap = BlockMap{q.h * q.wd, 1, (int32_t)q.p[2], (int32_t)q.p[3], (int32_t)q.p[1], (int32_t)q.wd, 0};
+            a.ymap = BlockMap{q.h * q.wd, 1, (int32_t)q.p[2], (int32_t)q.p[3], (int32_t)q.p[1], (int32_t)q.wd,
+                              sp.rperm >= 0 ? 1 : 0};
             set_args(l, a);
             return {l};
         }
-        std::vector<Launch> v{sp.epi ? with_epilogue(sp, g, base, sp.pout) : base};
+        // no map: the residual is the permutation's output after all
+        StepSpec s2 = sp;
+        if (sp.rperm >= 0) {
+            s2.r1 = sp.r1p;
+            restore_perm(sp.rperm);
+        }
+        std::vector<Launch> v{s2.epi ? with_epilogue(s2, g, base, s2.pout) : base};
         for (const Launch &x : ops[sp.perm]) v.push_back(x);
         return v;
+    };
+    // A GateMm reading an elided forward permutation's source through the
+    // token map (the streaming kernels' _xm form, layout by mode), or, where
+    // the producer is not one of them, the permutation after all.
+    auto token_map = [&](const StepSpec &sp, Launch &l) {
+        const mx_op &o = p->ops[sp.first], &q = p->ops[sp.xperm];
+        const char *want = o.mode == 0 ? "mx_pw_ch" : "mx_pw_rw";
+        if (strncmp(l.name, want, 8) || !aligned(dev(sp.xsrc), 16)) {
+            restore_perm(sp.xperm);
+            return;
+        }
+        const std::string nm = l.name;
+        const bool f = nm.size() > 2 && nm.compare(nm.size() - 2, 2, "_f") == 0;
+        l.name = intern((f ? nm.substr(0, nm.size() - 2) : nm) + "_xm" + (f ? "_f" : ""));
+        l.f = fn(l.name);
+        GemmArgs a;
+        memcpy(&a, l.a0, sizeof a);
+        a.B = dev(sp.xsrc);
+        a.xmap = BlockMap{q.h * q.wd, 1, (int32_t)q.p[2], (int32_t)q.p[3], (int32_t)q.p[1], (int32_t)q.wd, 0};
+        set_args(l, a);
     };
     prog.clear();
     for (const StepSpec &sp : pg.specs) {
         if (sp.rule == RULE_ELIDED) {
+            prog.push_back(Step{sp.first, sp.last, {}});
+            continue;
+        }
+        if (sp.rule == RULE_PERM_IN) {
+            perm_step[sp.first] = (int64_t)prog.size();
             prog.push_back(Step{sp.first, sp.last, {}});
             continue;
         }
@@ -1563,8 +1704,9 @@ void Gpu::build_program(const mx_plan_desc *p) {
             continue;
         }
         if (sp.ln < 0) {
-            if (sp.out < 0) prog.push_back(Step{sp.first, sp.last, ops[sp.first]});
-            else prog.push_back(Step{sp.first, sp.last, gemm_part(sp, sp.first)});
+            std::vector<Launch> v = sp.out < 0 ? ops[sp.first] : gemm_part(sp, sp.first);
+            if (sp.xperm >= 0) token_map(sp, v[0]);
+            prog.push_back(Step{sp.first, sp.last, v});
             continue;
         }
         // A LayerNorm folded into the next op's streaming GEMM: the
@@ -1575,11 +1717,16 @@ void Gpu::build_program(const mx_plan_desc *p) {
         ChanLnArgs la;
         memcpy(&la, ops[sp.first][0].a0, sizeof la);
         float *stats = scratch + ln_off;
+        // an elided forward permutation: statistics and columns from its
+        // source in image order, the GEMM reading through the block map
+        const bool xmap = sp.xperm >= 0 && aligned(dev(sp.xsrc), 16);
+        if (xmap) la.x = dev(sp.xsrc);
         const bool ok = !strncmp(conv.name, "mx_pw_ch", 8) && aligned(la.x, 16) && la.hw % 4 == 0;
         std::vector<Launch> gp = gemm_part(sp, g);
         Launch &gl = gp[0];
-        if (!ok || strncmp(gl.name, "mx_pw_ch", 8)) {
+        if (!ok || strncmp(gl.name, "mx_pw_ch", 8) || (sp.xperm >= 0 && !xmap)) {
             // not streaming (shape or alignment): the LayerNorm runs on its own
+            restore_perm(sp.xperm);
             Step st{sp.first, sp.last, ops[sp.first]};
             st.main = st.launches.size();
             for (const Launch &x : gp) st.launches.push_back(x);
@@ -1607,6 +1754,10 @@ void Gpu::build_program(const mx_plan_desc *p) {
         memcpy(&a, gl.a0, sizeof a);
         a.B = la.x;
         a.ln = LnIn{stats, stats + ln.hw, la.scale, la.bias};
+        if (xmap) {
+            const mx_op &q = p->ops[sp.xperm];
+            a.xmap = BlockMap{q.h * q.wd, 1, (int32_t)q.p[2], (int32_t)q.p[3], (int32_t)q.p[1], (int32_t)q.wd, 0};
+        }
         set_args(gl, a);
         Step st{sp.first, sp.last, {sl}};
         for (const Launch &x : gp) st.launches.push_back(x);

@@ -128,15 +128,20 @@ struct LnIn {
     const float *mean, *rstd, *scale, *bias;
 };
 
-// A block permutation folded into a GEMM's stores (BlockPerm backward, no
-// swap, src/model.rs:104-106): output element e (counted from C) is written
-// at (e / plane) * plane + map(e % plane), where map takes the blocked index
-// g * fh * fw + fy * fw + fx (g = gy * gw + gx) to the image index
-// (gy * fh + fy) * wd + gx * fw + fx. fw % 4 == 0 keeps four consecutive
-// outputs contiguous.
+// A block permutation folded into a GEMM (BlockPerm, no swap,
+// src/model.rs:104-106). map takes the blocked index g * fh * fw + fy * fw + fx
+// (g = gy * gw + gx) to the image index (gy * fh + fy) * wd + gx * fw + fx;
+// fw % 4 == 0 keeps four consecutive elements contiguous.
+//   ymap (backward permutation of the output): output element e (counted
+//       from C) is written at (e / plane) * plane + map(e % plane); with
+//       r1map the epilogue's r1 is read at that same position, i.e. r1 is the
+//       image-ordered tensor whose blocked view the output is added to.
+//   xmap (forward permutation of the input, channel-major GEMMs with a
+//       folded LayerNorm): X column n is read at map(n) of the image-ordered
+//       tensor, and so are the LayerNorm statistics.
 struct BlockMap {
     int64_t plane;
-    int32_t on, fh, fw, gw, wd, pad;
+    int32_t on, fh, fw, gw, wd, r1map;
 };
 
 struct GemmArgs {
@@ -151,7 +156,7 @@ struct GemmArgs {
     int32_t cvec, pad;    // 1: C, u, r1, r2 are 16-byte aligned (128-bit stores)
     Epilogue e;
     LnIn ln;
-    BlockMap ymap;
+    BlockMap ymap, xmap;
 };
 
 // Small GEMV for the plane-1 CALayer convs: y[o] = b[o] + sum_i w[o][i] x[i].

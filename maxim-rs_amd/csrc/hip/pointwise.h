@@ -50,7 +50,17 @@ __device__ __forceinline__ float comp(const float4 &v, int t) {
 // that are never stored, so no branch or select sits between the loads and
 // the matrix cores. The reduction ping-pongs between two register buffers,
 // so the loads of superstep s + 1 are in flight while superstep s multiplies.
-template <int LAYOUT, int TMW, int KS, bool FUSED, bool LN>
+// The image index of blocked index e (0 <= e < plane) under map q (32-bit:
+// the host enables a map only below 2^31 elements).
+__device__ __forceinline__ uint32_t unblock(const BlockMap &q, uint32_t e) {
+    const uint32_t pp = (uint32_t)(q.fh * q.fw);
+    const uint32_t gi = e / pp, p = e - gi * pp;
+    const uint32_t gy = gi / (uint32_t)q.gw, gx = gi - gy * (uint32_t)q.gw;
+    const uint32_t fy = p / (uint32_t)q.fw, fx = p - fy * (uint32_t)q.fw;
+    return (gy * q.fh + fy) * q.wd + gx * q.fw + fx;
+}
+
+template <int LAYOUT, int TMW, int KS, bool FUSED, bool LN, bool XM = false>
 __device__ void body(const GemmArgs &a) {
     constexpr int TW = 16 * TMW;    // weight outputs per tile
     constexpr int NACC = 16 * TMW;  // accumulator floats per lane
@@ -66,7 +76,11 @@ __device__ void body(const GemmArgs &a) {
     const float *W = a.A + (int64_t)b * a.sA;
     const float *X = a.B + (int64_t)b * a.sB;
     float *Y = a.C + (int64_t)b * a.sC;
-    const int64_t xstep = LAYOUT == CH ? 16 * (int64_t)N : 16;  // one superstep
+    // X's advance per superstep (16 k's): 16 rows (CH) or 16 columns (RW);
+    // through a token map, whole rows of cells or of cell pixels.
+    const BlockMap &xm = a.xmap;
+    int64_t xstep = LAYOUT == CH ? 16 * (int64_t)N : 16;
+    if (XM) xstep = LAYOUT == CH ? (int64_t)(16 / xm.gw) * xm.fh * xm.wd : (int64_t)(16 / xm.fw) * xm.wd;
 
     // One XCD per contiguous range of blocks, so neighbouring tiles (which
     // share operands) meet in the same L2.
@@ -86,13 +100,42 @@ __device__ void body(const GemmArgs &a) {
 #pragma unroll
     for (int mt = 0; mt < TMW; ++mt)
         wp[mt] = W + (int64_t)min(w0 + mt * 16 + i, wout - 1) * K + 4 * g + S0 * 16;
+    // Input maps: X as the blocked view of an image-ordered tensor (an
+    // elided forward permutation). With a folded LayerNorm (CH, xmap.on): X
+    // is [channels][pixels] and only the pixel axis is blocked. XM (GateMm):
+    // each batch's X is [cells][pixels of a cell] of one channel plane, so
+    // element (r, c) sits at cell(r) + pixel(c); the host guarantees that 16
+    // k's advance whole cell rows (CH: 16 % gw == 0) or whole pixel rows
+    // (RW: 16 % fw == 0), and fw % 4 == 0 for the 128-bit reads.
+    auto cell = [&](uint32_t r) -> int64_t {
+        const uint32_t gy = r / (uint32_t)xm.gw, gx = r - gy * (uint32_t)xm.gw;
+        return (int64_t)gy * xm.fh * xm.wd + (int64_t)gx * xm.fw;
+    };
+    auto pixel = [&](uint32_t c) -> int64_t {
+        const uint32_t fy = c / (uint32_t)xm.fw, fx = c - fy * (uint32_t)xm.fw;
+        return (int64_t)fy * xm.wd + fx;
+    };
+    // CH: this lane's four columns, s0 + 16 (i % 4) + 4 (i / 4) .. + 3
+    int xcol = 0;
+    if (LAYOUT == CH) {
+        xcol = min(s0 + 16 * (i & 3) + 4 * (i >> 2), N - 4);
+        if (LN && xm.on) xcol = (int)unblock(xm, (uint32_t)xcol);
+    }
     const float *xp[4];
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
-        if (LAYOUT == CH)  // row k = 16 S + 4 g + q, elements s0 + 16 (i % 4) + 4 (i / 4) .. + 3
-            xp[q] = X + (int64_t)(4 * g + q) * N + min(s0 + 16 * (i & 3) + 4 * (i >> 2), N - 4) + S0 * xstep;
-        else               // row s0 + 16 q + i, k = 16 S + 4 g .. + 3
-            xp[q] = X + (int64_t)min(s0 + 16 * q + i, M - 1) * K + 4 * g + S0 * xstep;
+        if (LAYOUT == CH) {  // row k = 16 S + 4 g + q
+            if (XM)
+                xp[q] = X + cell(16 * S0 + 4 * g + q) + pixel(xcol);
+            else
+                xp[q] = X + (int64_t)(4 * g + q) * N + xcol + S0 * xstep;
+        } else {  // row s0 + 16 q + i, k = 16 S + 4 g .. + 3
+            const int row = min(s0 + 16 * q + i, M - 1);
+            if (XM)
+                xp[q] = X + cell(row) + pixel(16 * S0 + 4 * g);
+            else
+                xp[q] = X + (int64_t)row * K + 4 * g + S0 * xstep;
+        }
     }
 
     f32x4 acc[4][TMW];
@@ -105,10 +148,9 @@ __device__ void body(const GemmArgs &a) {
     // the whole tile, and each superstep's scale/bias for k = 16 S + 4 g + q.
     float4 lmean, lrstd;
     const float *lsc = nullptr, *lbi = nullptr;
-    if (LN) {  // a single 1x1 conv (no batch): pixel n's statistics at n
-        const int n = min(s0 + 16 * (i & 3) + 4 * (i >> 2), N - 4);
-        lmean = ld4(a.ln.mean + n);
-        lrstd = ld4(a.ln.rstd + n);
+    if (LN) {  // a single 1x1 conv (no batch): statistics indexed like X's columns
+        lmean = ld4(a.ln.mean + xcol);
+        lrstd = ld4(a.ln.rstd + xcol);
         lsc = a.ln.scale + 4 * g + S0 * 16;
         lbi = a.ln.bias + 4 * g + S0 * 16;
     }
@@ -197,13 +239,21 @@ __device__ void body(const GemmArgs &a) {
     // The fused epilogue's operands are fetched one slot ahead, so their
     // latency overlaps the previous slot's arithmetic and store (the
     // compiler cannot move a load above a store that might alias it).
+    // Where output element off (counted from this batch's Y) is stored: off
+    // itself, or its image position under a folded backward permutation.
+    auto placed = [&](int64_t off) -> int64_t {
+        if (!a.ymap.on) return off;
+        const uint32_t e = (uint32_t)(cbase + off), pl = (uint32_t)a.ymap.plane;
+        const uint32_t base = e / pl * pl;
+        return (int64_t)(base + unblock(a.ymap, e - base)) - cbase;
+    };
     float4 ou[2], o1[2], o2[2];
     auto operands = [&](int k, int buf) {
         int64_t off;
         const bool ok = where(k, off);
         const int64_t at = cbase + (ok ? off : 0);
         if (a.e.u) ou[buf] = ld4(a.e.u + at);
-        if (a.e.r1) o1[buf] = ld4(a.e.r1 + at);
+        if (a.e.r1) o1[buf] = ld4(a.e.r1 + (a.ymap.r1map ? cbase + placed(ok ? off : 0) : at));
         if (a.e.r2) o2[buf] = ld4(a.e.r2 + at);
     };
     if (FUSED) operands(0, 0);
@@ -269,36 +319,27 @@ __device__ void body(const GemmArgs &a) {
                 v[3] = v[3] + o2[bi].w;
             }
         }
-        int64_t at = off;
-        if (a.ymap.on) {  // a folded block permutation: the image position
-            // (32-bit: the host enables the map only below 2^31 elements)
-            const BlockMap &q = a.ymap;
-            const uint32_t e = (uint32_t)(b * a.sC + off), pl = (uint32_t)q.plane;
-            const uint32_t base = e / pl * pl, idx = e - base, pp = (uint32_t)(q.fh * q.fw);
-            const uint32_t gi = idx / pp, p = idx - gi * pp;
-            const uint32_t gy = gi / (uint32_t)q.gw, gx = gi - gy * (uint32_t)q.gw;
-            const uint32_t fy = p / (uint32_t)q.fw, fx = p - fy * (uint32_t)q.fw;
-            at = (int64_t)(base + (gy * q.fh + fy) * q.wd + gx * q.fw + fx) - b * a.sC;
-        }
-        st4(Y + at, make_float4(v[0], v[1], v[2], v[3]));
+        st4(Y + placed(off), make_float4(v[0], v[1], v[2], v[3]));
     }
 }
 
 }  // namespace pw
 
-// mx_pw_{ch,rw}<TMW>[_k4][_ln][_f]: 256 threads; _k4 splits the reduction
-// over the block's four waves, _ln folds a channel LayerNorm into X (CH only),
-// _f applies the fused epilogue.
-#define MXK_PW1(LNAME, LAYOUT, TMW, KS, LN, SUF)                                                   \
+// mx_pw_{ch,rw}<TMW>[_k4][_ln|_xm][_f]: 256 threads; _k4 splits the
+// reduction over the block's four waves, _ln folds a channel LayerNorm into X
+// (CH only), _xm reads X through a token map (GateMm over an elided forward
+// permutation), _f applies the fused epilogue.
+#define MXK_PW1(LNAME, LAYOUT, TMW, KS, LN, XM, SUF)                                               \
     extern "C" __global__ __launch_bounds__(256) void mx_pw_##LNAME##TMW##SUF(GemmArgs a) {        \
-        pw::body<pw::LAYOUT, TMW, KS, false, LN>(a);                                               \
+        pw::body<pw::LAYOUT, TMW, KS, false, LN, XM>(a);                                           \
     }                                                                                               \
     extern "C" __global__ __launch_bounds__(256) void mx_pw_##LNAME##TMW##SUF##_f(GemmArgs a) {    \
-        pw::body<pw::LAYOUT, TMW, KS, true, LN>(a);                                                \
+        pw::body<pw::LAYOUT, TMW, KS, true, LN, XM>(a);                                            \
     }
-#define MXK_PW(LNAME, LAYOUT, TMW) \
-    MXK_PW1(LNAME, LAYOUT, TMW, 1, false, ) MXK_PW1(LNAME, LAYOUT, TMW, 4, false, _k4)
-#define MXK_PW_LN(TMW) MXK_PW1(ch, CH, TMW, 1, true, _ln) MXK_PW1(ch, CH, TMW, 4, true, _k4_ln)
+#define MXK_PW(LNAME, LAYOUT, TMW)                                                                 \
+    MXK_PW1(LNAME, LAYOUT, TMW, 1, false, false, ) MXK_PW1(LNAME, LAYOUT, TMW, 4, false, false, _k4) \
+    MXK_PW1(LNAME, LAYOUT, TMW, 1, false, true, _xm) MXK_PW1(LNAME, LAYOUT, TMW, 4, false, true, _k4_xm)
+#define MXK_PW_LN(TMW) MXK_PW1(ch, CH, TMW, 1, true, false, _ln) MXK_PW1(ch, CH, TMW, 4, true, false, _k4_ln)
 MXK_PW(ch, CH, 1)
 MXK_PW(ch, CH, 2)
 MXK_PW(ch, CH, 4)

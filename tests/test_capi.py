@@ -55,6 +55,8 @@ def test_the_code_object_is_embedded_and_complete():
     launched |= {"mx_pw_%s%d%s%s" % (l, t, k, f) for l in ("ch", "rw") for t in (1, 2, 4)
                  for k in ("", "_k4") for f in ("", "_f")}
     launched |= {"mx_pw_ch%d%s_ln%s" % (t, k, f) for t in (1, 2, 4) for k in ("", "_k4") for f in ("", "_f")}
+    launched |= {"mx_pw_%s%d%s_xm%s" % (l, t, k, f) for l in ("ch", "rw") for t in (1, 2, 4)
+                 for k in ("", "_k4") for f in ("", "_f")}
     launched |= {"mx_c3_m%d_t%d%s" % (m, t, f) for m, t in ((32, 8), (64, 4)) for f in ("", "_f")}
     launched = {k for k in launched if not k.endswith("_")}
     missing = [k for k in sorted(launched) if k.encode() + b"\0" not in data]

@@ -238,3 +238,77 @@ def test_block_permutation_folded_into_the_stores(gpu_ok, kind, fw, misalign):
     else:
         assert steps[-1][:2] == (n - 1, n) and steps[-1][2].startswith("mx_block_perm"), steps
     check(got, oracle_plan(cp, inputs, Y), "%s -> block_perm, fw %d, misaligned %d" % (kind, fw, misalign))
+
+
+def elide_case(kind, gh, gw, fh, fw, c=32):
+    """A forward BlockPerm S -> P whose readers take S in image order through
+    the block map, so the permutation launches nothing:
+      "ln"    the gMLP branch: P -> LayerNorm -> conv1x1 -> gelu -> conv1x1
+              + P (residual) -> backward BlockPerm into S, then S copied out;
+      "gate0" / "gate1"  the cross-gating: P -> GateMm (mode 0 / 1) ->
+              backward BlockPerm to the image."""
+    from maxim_amd import plan as P
+    h, w = gh * fh, gw * fw
+    G, Pp = gh * gw, fh * fw
+    rng = np.random.default_rng(gh * 100 + fw + len(kind))
+    img, bl = (c, h, w), (c, G, Pp)
+    x = rng.standard_normal(img).astype(np.float32)
+    fwd = dict(c=c, h=h, wd=w, mode=P.PERM_FORWARD, p=[gh, gw, fh, fw])
+    bwd = dict(c=c, h=h, wd=w, mode=0, p=[gh, gw, fh, fw])
+    if kind == "ln":
+        c2, n = 2 * c, c * G * Pp
+        bufs = [img, bl, bl, (c2, G, Pp), (c2, G, Pp), bl, bl, img]
+        S, Pb, L, T, U, V, Z, O = range(8)
+        wts = [(1.0 + 0.1 * rng.standard_normal(c)).astype(np.float32), (0.1 * rng.standard_normal(c)).astype(np.float32),
+               he(rng, (c2, c), c), (0.1 * rng.standard_normal(c2)).astype(np.float32),
+               he(rng, (c, c2), c2), (0.1 * rng.standard_normal(c)).astype(np.float32)]
+        ops = [P.make_op(P.BLOCK_PERM, dst=Pb, src=S, **fwd),
+               P.make_op(P.CHAN_LN, dst=L, src=Pb, scale=0, bias=1, c=c, hw=G * Pp),
+               P.make_op(P.CONV1X1, dst=T, src=L, w=2, bias=3, c_in=c, c_out=c2, h=G, wd=Pp),
+               P.make_op(P.GELU, dst=U, src=T, n=2 * n),
+               P.make_op(P.CONV1X1, dst=V, src=U, w=4, bias=5, c_in=c2, c_out=c, h=G, wd=Pp),
+               P.make_op(P.ADD, dst=Z, src=V, src2=Pb, n=n),
+               P.make_op(P.BLOCK_PERM, dst=S, src=Z, **bwd),
+               P.make_op(P.COPY, dst=O, src=S, n=n)]
+    else:
+        mode = 0 if kind == "gate0" else 1
+        k = G if mode == 0 else Pp
+        bufs = [img, bl, bl, img]
+        S, Pb, T, O = range(4)
+        wts = [he(rng, (k, k), k), (rng.standard_normal(k) * 0.1).astype(np.float32)]
+        ops = [P.make_op(P.BLOCK_PERM, dst=Pb, src=S, **fwd),
+               P.make_op(P.GATE_MM, dst=T, src=Pb, w=0, bias=1, c=c, mode=mode, p=[G, Pp]),
+               P.make_op(P.BLOCK_PERM, dst=O, src=T, **bwd)]
+    cp = P.CustomPlan(bufs, ops, wts, input=S, output=O)
+    return cp, {S: x}, O
+
+
+@pytest.mark.parametrize("kind,gh,gw,fh,fw", [
+    ("ln", 4, 4, 8, 8),        # 16 cells of 8x8 (the low-resolution block gMLP)
+    ("ln", 2, 2, 12, 20),      # grid gMLP shape class: cells 12x20
+    ("ln", 3, 5, 4, 12),       # 15 cells, 48-pixel cells: ragged tiles
+    ("gate0", 16, 16, 2, 4),   # mode 0 over 256 cells (16 k's = one cell row)
+    ("gate0", 8, 8, 3, 8),     # 8-wide grid: 16 k's = two cell rows
+    ("gate1", 5, 7, 16, 16),   # mode 1 over 16x16 cells
+    ("gate1", 6, 4, 8, 8),     # 8x8 cells: 16 k's = two pixel rows
+])
+def test_forward_permutation_elided(gpu_ok, kind, gh, gw, fh, fw):
+    """The permutation's step launches nothing; the result matches the CPU
+    path and is bitwise the unfused pass (which runs the permutation)."""
+    from maxim_amd import hip as H
+    cp, inputs, out = elide_case(kind, gh, gw, fh, fw)
+    got, steps = run_plan(cp, inputs, out)
+    print("steps", steps)
+    gpu = H.Gpu(cp)
+    kern = {st: k for st, k in gpu.launches()}
+    first = [s for s, (a, b, _) in enumerate(steps) if a == 0][0]
+    assert first not in kern, "the forward permutation still launches: %s" % steps
+    assert any(k.endswith(("_xm", "_xm_f")) or "_ln" in k for k in kern.values()), kern
+    for b, v in inputs.items():
+        gpu.write_buf(b, v)
+    gpu.set_fusion(False)
+    gpu.run_ops(0, len(cp.ops))
+    plain = gpu.read_buf(out).reshape(got.shape)
+    gpu.close()
+    assert np.array_equal(got.view(np.uint32), plain.view(np.uint32)), "fused and unfused passes differ"
+    check(got, oracle_plan(cp, inputs, out), "%s perm elided %dx%d cells of %dx%d" % (kind, gh, gw, fh, fw))
