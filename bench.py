@@ -52,8 +52,8 @@ def smooth_image(h, w, seed=0, noise=0.1):
 
 def family(kernel):
     """Group kernel entry points into the family a roofline is quoted for."""
-    for pre in ("mx_gemm", "mx_pw", "mx_conv3x3", "mx_conv4x4", "mx_chan_ln", "mx_block_perm", "mx_resize",
-                "mx_chan_mean", "mx_gemv"):
+    for pre in ("mx_gemm", "mx_pw", "mx_conv3x3", "mx_c3", "mx_conv4x4", "mx_chan_ln", "mx_block_perm",
+                "mx_resize", "mx_chan_mean", "mx_ca", "mx_gemv"):
         if kernel.startswith(pre):
             return pre
     return kernel.rsplit("_", 1)[0] if kernel.endswith(("_v4", "_s")) else kernel
@@ -222,7 +222,8 @@ def launch_costs(plan, steps, launches, R):
     writes and reads back; the steps of several launches are split by kernel:
     a folded LayerNorm's statistics pass (reads x, writes mean and 1/std) and
     the GEMM that re-reads x with them, the two resize passes through `tmp`,
-    and the channel mean's partial and final sums."""
+    the channel mean's partial and final sums, and the partial sums before
+    the CALayer block that finishes the means."""
     def step_cost(a, b):
         f = sum(R.op_cost(plan.ops[k])[0] for k in range(a, b))
         by = sum(R.op_cost(plan.ops[k])[1] for k in range(a, b))
@@ -252,10 +253,13 @@ def launch_costs(plan, steps, launches, R):
                 out[i] = (0, 4 * (o.c * o.h * o.wd + o.c * o.h * o.ow))
             elif kn == "mx_resize_v":
                 out[i] = (0, 4 * (o.c * o.h * o.ow + o.c * o.oh * o.ow))
-            elif kn == "mx_chan_mean_part":
+            elif kn.startswith("mx_chan_mean_part"):
                 out[i] = (0, 4 * o.c * o.hw)
             elif kn == "mx_chan_mean_final":
                 out[i] = (0, 4 * o.c)
+            elif kn == "mx_ca_mean_mlp":  # the means finished, then the CALayer MLP
+                f, by = step_cost(a + 1, b)
+                out[i] = (f, by + 4 * o.c)
             else:  # the GEMM after an unfolded LayerNorm
                 out[i] = step_cost(a + 1, b)
     return out

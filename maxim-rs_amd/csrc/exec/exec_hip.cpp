@@ -132,6 +132,10 @@ struct ResizeTab {
     int32_t maxt, pad;
 };
 
+// Channel-mean partial sums: chunks of a multiple of 1024 elements (the
+// 128-bit kernel's stride), about 64 per channel, at least 2048 elements.
+int64_t mean_chunk(int64_t hw) { return std::max<int64_t>(2048, ((hw + 63) / 64 + 1023) / 1024 * 1024); }
+
 // The one-pass resize stages, per block of `rows` output rows, the input rows
 // from the first row's first vertical tap to the last row's last one. Returns
 // the most any block needs, or -1 if some row of a block reaches outside that
@@ -624,8 +628,8 @@ Gpu::Gpu(const mx_plan_desc *p) : H(hip()), doff(pg.doff) {
                 as_is(o.bias);
                 break;
             case MX_OP_CHAN_MEAN: {
-                int64_t chunk = std::max<int64_t>(2048, ((o.hw + 63) / 64 + 255) / 256 * 256);
-                int64_t nchunk = (o.hw + chunk - 1) / chunk;
+                const int64_t chunk = mean_chunk(o.hw);
+                const int64_t nchunk = (o.hw + chunk - 1) / chunk;
                 mean_scratch = std::max<uint64_t>(mean_scratch, (uint64_t)(o.c * nchunk));
                 break;
             }
@@ -829,10 +833,11 @@ void Gpu::build_launches(const mx_plan_desc *p, const std::vector<int64_t> &woff
                 break;
             }
             case MX_OP_CHAN_MEAN: {
-                int64_t chunk = std::max<int64_t>(2048, ((o.hw + 63) / 64 + 255) / 256 * 256);
-                int32_t nchunk = (int32_t)((o.hw + chunk - 1) / chunk);
+                const int64_t chunk = mean_chunk(o.hw);
+                const int32_t nchunk = (int32_t)((o.hw + chunk - 1) / chunk);
                 ChanMeanArgs a{B(o.src), scratch, B(o.dst), o.hw, chunk, (int32_t)o.c, nchunk};
-                Launch l1 = mk("mx_chan_mean_part");
+                const bool vec = o.hw % 4 == 0 && aligned(a.x, 16);
+                Launch l1 = mk(vec ? "mx_chan_mean_part4" : "mx_chan_mean_part");
                 l1.g[0] = (unsigned)nchunk;
                 l1.g[1] = grid_yz(o.c);
                 set_args(l1, a);
@@ -1323,18 +1328,27 @@ void Program::plan_fusion(const mx_plan_desc *p, bool require_clear) {
             continue;
         }
         // The CALayer's MLP: plane-1 Conv1x1 -> Lrelu -> plane-1 Conv1x1 ->
-        // Sigmoid, one block (mx_ca_mlp).
-        if (o.kind == MX_OP_CONV1X1 && o.h * o.wd == 1 && i + 3 < p->n_ops && o.c_out <= 1024) {
-            const mx_op &n1 = p->ops[i + 1], &n2 = p->ops[i + 2], &n3 = p->ops[i + 3];
-            if (n1.kind == MX_OP_LRELU && n1.src == o.dst && n1.n == o.c_out && n2.kind == MX_OP_CONV1X1 &&
-                n2.h * n2.wd == 1 && n2.src == n1.dst && n2.c_in == o.c_out && n2.c_out == o.c_in &&
-                n3.kind == MX_OP_SIGMOID && n3.src == n2.dst && n3.n == n2.c_out && only_reader(o.dst, i, i + 1) &&
-                only_reader(n1.dst, i + 1, i + 2) && only_reader(n2.dst, i + 2, i + 3) &&
-                clear_of(n3.dst, {o.src})) {
-                sp.rule = RULE_CA_MLP;
-                sp.out = n3.dst;
-                sp.last = i + 4;
-            }
+        // Sigmoid, one block (mx_ca_mlp); with the ChanMean before it, that
+        // block also finishes the means (mx_ca_mean_mlp).
+        auto ca_mlp_at = [&](uint64_t k) {
+            if (k + 3 >= p->n_ops) return false;
+            const mx_op &c1 = p->ops[k], &n1 = p->ops[k + 1], &n2 = p->ops[k + 2], &n3 = p->ops[k + 3];
+            return c1.kind == MX_OP_CONV1X1 && c1.h * c1.wd == 1 && c1.c_out <= 1024 && c1.c_in <= 1024 &&
+                   n1.kind == MX_OP_LRELU && n1.src == c1.dst && n1.n == c1.c_out && n2.kind == MX_OP_CONV1X1 &&
+                   n2.h * n2.wd == 1 && n2.src == n1.dst && n2.c_in == c1.c_out && n2.c_out == c1.c_in &&
+                   n3.kind == MX_OP_SIGMOID && n3.src == n2.dst && n3.n == n2.c_out && only_reader(c1.dst, k, k + 1) &&
+                   only_reader(n1.dst, k + 1, k + 2) && only_reader(n2.dst, k + 2, k + 3) && clear_of(n3.dst, {c1.src});
+        };
+        if (o.kind == MX_OP_CHAN_MEAN && o.c <= 1024 && i + 1 < p->n_ops && p->ops[i + 1].src == o.dst &&
+            p->ops[i + 1].c_in == o.c && ca_mlp_at(i + 1) && only_reader(o.dst, i, i + 1) &&
+            clear_of(p->ops[i + 4].dst, {o.src, o.dst})) {
+            sp.rule = RULE_CA_MLP;
+            sp.out = p->ops[i + 4].dst;
+            sp.last = i + 5;
+        } else if (o.kind == MX_OP_CONV1X1 && ca_mlp_at(i)) {
+            sp.rule = RULE_CA_MLP;
+            sp.out = p->ops[i + 3].dst;
+            sp.last = i + 4;
         }
         // ChanScale -> Add: y = x * s + r in one pass.
         if (sp.rule == RULE_NONE && o.kind == MX_OP_CHAN_SCALE && i + 1 < p->n_ops) {
@@ -1681,13 +1695,25 @@ void Gpu::build_program(const mx_plan_desc *p) {
             continue;
         }
         if (sp.rule == RULE_CA_MLP) {
+            const bool mean = p->ops[sp.first].kind == MX_OP_CHAN_MEAN;
+            const uint64_t c1 = sp.first + (mean ? 1 : 0);
             GemvArgs g1, g2;
-            memcpy(&g1, ops[sp.first][0].a0, sizeof g1);
-            memcpy(&g2, ops[sp.first + 2][0].a0, sizeof g2);
-            CaArgs a{g1.x, g1.w, g1.bias, g2.w, g2.bias, dev(sp.out), g1.ci, g1.co, p->ops[sp.first + 1].slope, 0};
-            Launch l = mk("mx_ca_mlp");
-            set_args(l, a);
-            prog.push_back(Step{sp.first, sp.last, {l}});
+            memcpy(&g1, ops[c1][0].a0, sizeof g1);
+            memcpy(&g2, ops[c1 + 2][0].a0, sizeof g2);
+            CaArgs a{g1.x, g1.w, g1.bias, g2.w, g2.bias, dev(sp.out), g1.ci, g1.co, p->ops[c1 + 1].slope, 0};
+            if (!mean) {
+                Launch l = mk("mx_ca_mlp");
+                set_args(l, a);
+                prog.push_back(Step{sp.first, sp.last, {l}});
+                continue;
+            }
+            // the ChanMean's partial sums, then the means and the MLP in one block
+            ChanMeanArgs m;
+            memcpy(&m, ops[sp.first][0].a0, sizeof m);
+            CaMeanArgs cm{a, m.part, m.y, m.hw, m.nchunk, 0};
+            Launch l = mk("mx_ca_mean_mlp");
+            set_args(l, cm);
+            prog.push_back(Step{sp.first, sp.last, {ops[sp.first][0], l}});
             continue;
         }
         if (sp.rule == RULE_SCALE_ADD) {

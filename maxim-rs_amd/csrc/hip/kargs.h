@@ -41,6 +41,17 @@ struct CaArgs {
     int32_t pad;
 };
 
+// The CALayer's global average pool finished in the MLP's block: the
+// channel means from mx_chan_mean_part's partial sums (mx_chan_mean_final's
+// order), kept in LDS for the MLP and also written to `mean`.
+struct CaMeanArgs {
+    CaArgs mlp;        // mlp.x unused: the means are computed here
+    const float *part;
+    float *mean;
+    int64_t hw;
+    int32_t nchunk, pad;
+};
+
 // Channel LayerNorm over [c][hw].
 struct ChanLnArgs {
     const float *x;

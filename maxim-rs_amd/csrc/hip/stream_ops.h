@@ -143,12 +143,12 @@ extern "C" __global__ __launch_bounds__(MXK_BLOCK) void mx_chan_scale_add_s(Chan
 // ReLU, then the sigmoid) in one block, with mx_gemv's summation order (bias
 // first, inputs ascending) and the elementwise kernels' expressions, so the
 // result is that of the four unfused launches to the bit.
-extern "C" __global__ __launch_bounds__(MXK_BLOCK) void mx_ca_mlp(CaArgs a) {
+__device__ __forceinline__ void ca_mlp_body(const CaArgs &a, const float *x) {
     __shared__ float h[1024];
     for (int j = threadIdx.x; j < a.r; j += MXK_BLOCK) {
         const float *w = a.w1 + (int64_t)j * a.c;
         float acc = a.b1 ? a.b1[j] : 0.0f;
-        for (int i = 0; i < a.c; ++i) acc += w[i] * a.x[i];
+        for (int i = 0; i < a.c; ++i) acc += w[i] * x[i];
         h[j] = acc >= 0.0f ? acc : a.slope * acc;
     }
     __syncthreads();
@@ -158,6 +158,26 @@ extern "C" __global__ __launch_bounds__(MXK_BLOCK) void mx_ca_mlp(CaArgs a) {
         for (int j = 0; j < a.r; ++j) acc += w[j] * h[j];
         a.y[o] = 1.0f / (1.0f + expf(-acc));
     }
+}
+
+extern "C" __global__ __launch_bounds__(MXK_BLOCK) void mx_ca_mlp(CaArgs a) { ca_mlp_body(a, a.x); }
+
+// Channel means (mx_chan_mean_final's ordered sum of the partials and its
+// division) straight into the MLP: one launch fewer, and the means never
+// leave the block before the MLP reads them (c <= 1024, checked by the host).
+extern "C" __global__ __launch_bounds__(MXK_BLOCK) void mx_ca_mean_mlp(CaMeanArgs a) {
+    __shared__ float xm[1024];
+    for (int ch = threadIdx.x; ch < a.mlp.c; ch += MXK_BLOCK) {
+        const float *p = a.part + (int64_t)ch * a.nchunk;
+        float s = 0.0f;
+#pragma unroll 8
+        for (int k = 0; k < a.nchunk; ++k) s += p[k];
+        const float m = s / (float)a.hw;
+        xm[ch] = m;
+        a.mean[ch] = m;
+    }
+    __syncthreads();
+    ca_mlp_body(a.mlp, xm);
 }
 
 // ------------------------------------------------------------ LayerNorm
@@ -334,10 +354,32 @@ extern "C" __global__ __launch_bounds__(MXK_BLOCK) void mx_chan_mean_part(ChanMe
     if (threadIdx.x == 0) a.part[(int64_t)ch * a.nchunk + k] = red[0];
 }
 
+// The same partial sums with 128-bit loads, for planes whose length is a
+// multiple of 4 and chunks of a multiple of 1024 elements: each thread adds
+// four consecutive elements, then every 1024th float4, and the block reduces
+// by a fixed butterfly within each wave and an ordered sum of the four waves.
+extern "C" __global__ __launch_bounds__(MXK_BLOCK) void mx_chan_mean_part4(ChanMeanArgs a) {
+    __shared__ float red[MXK_BLOCK / 64];
+    const int ch = blockIdx.y, k = blockIdx.x;
+    const float *x = a.x + (int64_t)ch * a.hw;
+    const int64_t lo = (int64_t)k * a.chunk, hi = lo + a.chunk < a.hw ? lo + a.chunk : a.hw;
+    float s = 0.0f;
+    for (int64_t i = lo + 4 * threadIdx.x; i < hi; i += 4 * MXK_BLOCK) {
+        const float4 v = ld4(x + i);
+        s += ((v.x + v.y) + v.z) + v.w;
+    }
+#pragma unroll
+    for (int w = 32; w > 0; w >>= 1) s += __shfl_xor(s, w);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = s;
+    __syncthreads();
+    if (threadIdx.x == 0) a.part[(int64_t)ch * a.nchunk + k] = ((red[0] + red[1]) + red[2]) + red[3];
+}
+
 extern "C" __global__ __launch_bounds__(MXK_BLOCK) void mx_chan_mean_final(ChanMeanArgs a) {
     const int ch = blockIdx.x * MXK_BLOCK + threadIdx.x;
     if (ch >= a.c) return;
     float s = 0.0f;
+#pragma unroll 8
     for (int k = 0; k < a.nchunk; ++k) s += a.part[(int64_t)ch * a.nchunk + k];
     a.y[ch] = s / (float)a.hw;
 }
