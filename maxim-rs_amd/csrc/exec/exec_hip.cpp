@@ -132,6 +132,21 @@ struct ResizeTab {
     int32_t maxt, pad;
 };
 
+// The LayerNorm tile kernel for c in {32, 64, 128}: c x P pixels per block,
+// the widest P (up to 8192 / c) that still gives four blocks per CU (two at
+// 128 channels, whose longer serial pass favours wider tiles), else the
+// narrowest: the serial channel pass of a block is latency-bound, so small
+// planes want more blocks (measured at C4). Returns the pixels per block and
+// the name suffix.
+std::pair<int64_t, std::string> ln_tile(int64_t c, int64_t hw, int cus) {
+    const int64_t want = (c >= 128 ? 2LL : 4LL) * (cus > 0 ? cus : 256);
+    const int64_t full = 8192 / c;
+    for (int64_t pp : {full, full / 2, full / 4})
+        if ((hw + pp - 1) / pp >= want || pp == full / 4)
+            return {pp, pp == full ? std::string() : "_p" + std::to_string(pp)};
+    return {full, std::string()};
+}
+
 // Channel-mean partial sums: chunks of a multiple of 1024 elements (the
 // 128-bit kernel's stride), about 64 per channel, at least 2048 elements.
 int64_t mean_chunk(int64_t hw) { return std::max<int64_t>(2048, ((hw + 63) / 64 + 1023) / 1024 * 1024); }
@@ -823,10 +838,13 @@ void Gpu::build_launches(const mx_plan_desc *p, const std::vector<int64_t> &woff
                 const char *k = "mx_chan_ln_any";
                 int64_t per = MXK_BLOCK;  // pixels per block
                 const bool vec = o.hw % 4 == 0 && aligned(a.x, 16) && aligned(a.y, 16);
-                if (vec && o.c == 32) { k = "mx_chan_ln_c32"; per = 256; }
-                else if (vec && o.c == 64) { k = "mx_chan_ln_c64"; per = 128; }
-                else if (vec && o.c == 128) { k = "mx_chan_ln_c128"; per = 64; }
-                Launch l = mk(k);
+                std::string kn = k;
+                if (vec && (o.c == 32 || o.c == 64 || o.c == 128)) {
+                    const auto t = ln_tile(o.c, o.hw, cus);
+                    kn = "mx_chan_ln_c" + std::to_string(o.c) + t.second;
+                    per = t.first;
+                }
+                Launch l = mk(kn);
                 l.g[0] = cdiv(o.hw, per);
                 set_args(l, a);
                 L.push_back(l);
@@ -1763,10 +1781,11 @@ void Gpu::build_program(const mx_plan_desc *p) {
         sa.y = stats;
         Launch sl;
         if (ln.c == 64 || ln.c == 128) {
-            // the LayerNorm kernels' LDS tile, C x (8192 / C) pixels per block
-            // (measured faster than the register loop from 64 channels up)
-            sl = mk(ln.c == 64 ? "mx_chan_ln_stats_c64" : "mx_chan_ln_stats_c128");
-            sl.g[0] = cdiv(ln.hw, 8192 / ln.c);
+            // the LayerNorm kernels' LDS tile (measured faster than the
+            // register loop from 64 channels up)
+            const auto t = ln_tile(ln.c, ln.hw, cus);
+            sl = mk("mx_chan_ln_stats_c" + std::to_string(ln.c) + t.second);
+            sl.g[0] = cdiv(ln.hw, t.first);
         } else {
             sl = mk("mx_chan_ln_stats");
             sl.g[0] = cdiv((ln.hw + 3) / 4, MXK_BLOCK);

@@ -197,7 +197,7 @@ extern "C" __global__ __launch_bounds__(MXK_BLOCK) void mx_ca_mean_mlp(CaMeanArg
 // y[hw .. 2 hw)), for a LayerNorm folded into the next op's GEMM.
 template <int C, int P, bool STATS = false>
 __device__ void chan_ln_tile(const ChanLnArgs &a) {
-    static_assert(C * P == 8192, "a 32 KiB tile");
+    static_assert(C * P <= 8192 && P % 4 == 0 && P <= MXK_BLOCK, "a tile of at most 32 KiB");
     __shared__ float t[C][P];
     __shared__ float st[2][P];
     const int tid = threadIdx.x;
@@ -264,9 +264,26 @@ __device__ void chan_ln_tile(const ChanLnArgs &a) {
 }
 
 // 128-bit paths need hw % 4 == 0 and 16-byte aligned x and y.
-extern "C" __global__ __launch_bounds__(MXK_BLOCK) void mx_chan_ln_c32(ChanLnArgs a) { chan_ln_tile<32, 256>(a); }
-extern "C" __global__ __launch_bounds__(MXK_BLOCK) void mx_chan_ln_c64(ChanLnArgs a) { chan_ln_tile<64, 128>(a); }
-extern "C" __global__ __launch_bounds__(MXK_BLOCK) void mx_chan_ln_c128(ChanLnArgs a) { chan_ln_tile<128, 64>(a); }
+// mx_chan_ln_c<C>[_p<P>] and mx_chan_ln_stats_c<C>[_p<P>]: C channels x P
+// pixels per block (P = 8192 / C without the suffix); the smaller tiles give
+// small planes more blocks, since each block's serial channel pass is
+// latency-bound.
+#define MXK_LN(C, P, SUF)                                                                           \
+    extern "C" __global__ __launch_bounds__(MXK_BLOCK) void mx_chan_ln_c##C##SUF(ChanLnArgs a) {    \
+        chan_ln_tile<C, P>(a);                                                                      \
+    }                                                                                               \
+    extern "C" __global__ __launch_bounds__(MXK_BLOCK) void mx_chan_ln_stats_c##C##SUF(ChanLnArgs a) { \
+        chan_ln_tile<C, P, true>(a);                                                                \
+    }
+MXK_LN(32, 256, )
+MXK_LN(32, 128, _p128)
+MXK_LN(32, 64, _p64)
+MXK_LN(64, 128, )
+MXK_LN(64, 64, _p64)
+MXK_LN(64, 32, _p32)
+MXK_LN(128, 64, )
+MXK_LN(128, 32, _p32)
+MXK_LN(128, 16, _p16)
 
 // Any channel count, any alignment: reads x twice.
 extern "C" __global__ __launch_bounds__(MXK_BLOCK) void mx_chan_ln_any(ChanLnArgs a) {
@@ -289,20 +306,11 @@ extern "C" __global__ __launch_bounds__(MXK_BLOCK) void mx_chan_ln_any(ChanLnArg
 }
 
 // The per-pixel statistics alone, for a LayerNorm folded into the following
-// 1x1 conv: chan_ln_tile's staging, sums, order and expressions, so the
-// normalised values the GEMM forms from them are that kernel's to the bit.
-extern "C" __global__ __launch_bounds__(MXK_BLOCK) void mx_chan_ln_stats_c32(ChanLnArgs a) {
-    chan_ln_tile<32, 256, true>(a);
-}
-extern "C" __global__ __launch_bounds__(MXK_BLOCK) void mx_chan_ln_stats_c64(ChanLnArgs a) {
-    chan_ln_tile<64, 128, true>(a);
-}
-extern "C" __global__ __launch_bounds__(MXK_BLOCK) void mx_chan_ln_stats_c128(ChanLnArgs a) {
-    chan_ln_tile<128, 64, true>(a);
-}
-
-// Any channel count: four pixels per thread, the channel loop in registers.
-// Needs hw % 4 == 0 and 16-byte aligned x and y.
+// 1x1 conv (the mx_chan_ln_stats_c* forms above use chan_ln_tile's staging,
+// sums, order and expressions, so the normalised values the GEMM forms from
+// them are that kernel's to the bit). This one takes any channel count: four
+// pixels per thread, the channel loop in registers. Needs hw % 4 == 0 and
+// 16-byte aligned x and y.
 extern "C" __global__ __launch_bounds__(MXK_BLOCK) void mx_chan_ln_stats(ChanLnArgs a) {
     const int64_t p = ((int64_t)blockIdx.x * MXK_BLOCK + threadIdx.x) * 4;
     if (p >= a.hw) return;
