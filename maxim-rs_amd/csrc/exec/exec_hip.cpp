@@ -1274,12 +1274,14 @@ void Program::plan_fusion(const mx_plan_desc *p, bool require_clear) {
     };
 
     // Copy elision (own device layout only): a copy whose source x has one
-    // writer and no other reader, and whose destination's bytes nothing
-    // touches between that writer and the copy, is served by laying x out on
-    // the destination's storage: the writer then produces the destination
-    // directly and the copy's step launches nothing (run op by op it copies
-    // the destination onto itself). Checked per storage owner (the view
-    // table's base), since the executor lays out every owner itself.
+    // writer, and whose destination's bytes nothing touches between that
+    // writer and the copy nor rewrites while x is still read after it, is
+    // served by laying x out on the destination's storage: the writer then
+    // produces the destination directly (x's other readers, e.g. a skip
+    // connection's, read it there) and the copy's step launches nothing (run
+    // op by op it copies the destination onto itself). Checked per storage
+    // owner (the view table's base), since the executor lays out every owner
+    // itself.
     elide_to.assign(p->n_bufs, -1);
     std::vector<char> elided(p->n_ops, 0);
     if (!require_clear) {
@@ -1311,19 +1313,29 @@ void Program::plan_fusion(const mx_plan_desc *p, bool require_clear) {
             const mx_op &c = p->ops[j];
             if (c.kind != MX_OP_COPY) continue;
             const int64_t x = c.src, d = c.dst;
-            if (x == d || base[x] != x || views[x] || writers[x] != 1 || target[x] || elide_to[d] >= 0) continue;
+            if (x == d || base[x] != x || views[x] || writers[x] != 1 || target[x] || elide_to[d] >= 0 ||
+                elide_to[x] >= 0)  // x copied twice: it takes the first destination only
+                continue;
             if ((uint64_t)x == p->input || (uint64_t)x == p->output || (p->keep && p->keep[x])) continue;
             if ((uint64_t)c.n != blen(x) || (uint64_t)c.n != blen(d)) continue;
             int64_t w = -1;  // x's writer
             for (uint64_t k = 0; k < j; ++k)
                 for (int64_t b : writes_of(p->ops[k]))
                     if (b == x) w = (int64_t)k;
-            if (w < 0 || !only_reader(x, (uint64_t)w, j)) continue;
+            if (w < 0) continue;
             bool ok = true;
-            for (uint64_t k = 0; k < (uint64_t)w && ok; ++k)  // nothing reads x before it is written
-                for (int64_t b : reads_of(p->ops[k])) ok = ok && b != x;
+            uint64_t last_read = j;  // x's last reader (x may have others: a skip connection)
+            for (uint64_t k = 0; k < p->n_ops; ++k)
+                for (int64_t b : reads_of(p->ops[k]))
+                    if (b == x) {
+                        if (k < (uint64_t)w) ok = false;  // nothing reads x before it is written
+                        last_read = std::max(last_read, k);
+                    }
             for (int64_t b : reads_of(p->ops[w])) ok = ok && !shares(b, d);  // the writer reads no byte of d
             for (uint64_t k = (uint64_t)w + 1; k < j && ok; ++k) ok = !touches(p->ops[k], d);
+            // d's bytes keep x's value for as long as x is read after the copy
+            for (uint64_t k = j + 1; k <= last_read && ok; ++k)
+                for (int64_t b : writes_of(p->ops[k])) ok = ok && !shares(b, d);
             if (!ok) continue;
             elide_to[x] = d;
             target[d] = 1;
@@ -1594,6 +1606,10 @@ void Program::layout(const mx_plan_desc *p, bool repack) {
     for (uint64_t i = 0; i < n; ++i) doff[i] = off[base[i]] + delta[i];
     arena_len = std::max<uint64_t>(total, 1);
     repacked = true;
+    // An elided copy launches nothing: its source must sit on its destination.
+    for (const StepSpec &sp : specs)
+        if (sp.rule == RULE_ELIDED && doff[p->ops[sp.first].src] != doff[p->ops[sp.first].dst])
+            throw Error("internal: an elided copy whose source is not laid out on its destination");
 }
 
 // Materialise the program: single-op steps reuse the op's launches; a fused
