@@ -274,6 +274,7 @@ struct StepSpec {
     // residual step reads r1 (then the source) at its stores' image positions
     // (r1p: the permutation's output, read instead if a kernel cannot map).
     int64_t xperm = -1, xsrc = -1, rperm = -1, r1p = -1;
+    int64_t xmul = -1;  // a Mul folded into the next op's GEMM operand (== first)
 };
 
 struct Program {
@@ -1203,6 +1204,7 @@ void Program::plan_fusion(const mx_plan_desc *p, bool require_clear) {
         const mx_op &n1 = p->ops[g + 1];
         std::vector<int64_t> reads = reads_of(o);
         if (sp.ln >= 0) reads.push_back(p->ops[sp.ln].src);
+        if (sp.xmul >= 0) for (int64_t r : reads_of(p->ops[sp.xmul])) reads.push_back(r);
         StepSpec f = sp;
         if (o.kind == MX_OP_GATE_MM && n1.kind == MX_OP_GATE_APPLY && n1.src2 == x && n1.src != x &&
             whole(n1, x)) {
@@ -1264,6 +1266,7 @@ void Program::plan_fusion(const mx_plan_desc *p, bool require_clear) {
         if (!only_reader(x, j - 1, j)) return;
         std::vector<int64_t> reads = reads_of(o);
         if (sp.ln >= 0) reads.push_back(p->ops[sp.ln].src);
+        if (sp.xmul >= 0) for (int64_t r : reads_of(p->ops[sp.xmul])) reads.push_back(r);
         for (int64_t r : {sp.u, sp.r1, sp.r2})
             if (r >= 0) reads.push_back(r);
         if (!clear_of(q.dst, reads)) return;
@@ -1407,7 +1410,20 @@ void Program::plan_fusion(const mx_plan_desc *p, bool require_clear) {
                 perm_out(i + 1, sp);
             }
         }
-        if (sp.rule == RULE_NONE && sp.ln < 0) {
+        // Mul -> 1x1 conv: the conv's streaming GEMM reads both factors and
+        // multiplies them on the way in (the _mul form).
+        if (sp.rule == RULE_NONE && sp.ln < 0 && o.kind == MX_OP_MUL && i + 1 < p->n_ops) {
+            const mx_op &n1 = p->ops[i + 1];
+            if (n1.kind == MX_OP_CONV1X1 && n1.src == o.dst && n1.h * n1.wd > 1 && whole(o, o.dst) &&
+                o.n == n1.c_in * n1.h * n1.wd && only_reader(o.dst, i, i + 1) &&
+                clear_of(n1.dst, {o.src, o.src2})) {
+                sp.xmul = (int64_t)i;
+                sp.last = i + 2;
+                epilogue(i + 1, sp);
+                perm_out(i + 1, sp);
+            }
+        }
+        if (sp.rule == RULE_NONE && sp.ln < 0 && sp.xmul < 0) {
             epilogue(i, sp);
             perm_out(i, sp);
         }
@@ -1761,6 +1777,33 @@ void Gpu::build_program(const mx_plan_desc *p) {
             l.g[1] = grid_yz(a.c);
             set_args(l, a);
             prog.push_back(Step{sp.first, sp.last, {l}});
+            continue;
+        }
+        if (sp.xmul >= 0) {
+            // the conv's GEMM reading both factors of the Mul, or, where it is
+            // not a streaming kernel (or the factors are misaligned), the Mul
+            // on its own before it
+            const uint64_t g = sp.first + 1;
+            const mx_op &m = p->ops[sp.first];
+            std::vector<Launch> v = sp.out < 0 ? ops[g] : gemm_part(sp, g);
+            Launch &l = v[0];
+            if (!strncmp(l.name, "mx_pw_ch", 8) && aligned(dev(m.src), 16) && aligned(dev(m.src2), 16)) {
+                const std::string nm = l.name;
+                const bool f = nm.size() > 2 && nm.compare(nm.size() - 2, 2, "_f") == 0;
+                l.name = intern((f ? nm.substr(0, nm.size() - 2) : nm) + "_mul" + (f ? "_f" : ""));
+                l.f = fn(l.name);
+                GemmArgs a;
+                memcpy(&a, l.a0, sizeof a);
+                a.B = dev(m.src);
+                a.B2 = dev(m.src2);
+                set_args(l, a);
+                prog.push_back(Step{sp.first, sp.last, v});
+            } else {
+                Step st{sp.first, sp.last, ops[sp.first]};
+                st.main = st.launches.size();
+                for (const Launch &x : v) st.launches.push_back(x);
+                prog.push_back(st);
+            }
             continue;
         }
         if (sp.ln < 0) {

@@ -168,6 +168,7 @@ struct GemmArgs {
     Epilogue e;
     LnIn ln;
     BlockMap ymap, xmap;
+    const float *B2;      // _mul: X is B * B2 elementwise (a folded Mul), same layout
 };
 
 // Small GEMV for the plane-1 CALayer convs: y[o] = b[o] + sum_i w[o][i] x[i].

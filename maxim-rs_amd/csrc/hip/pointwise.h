@@ -60,7 +60,7 @@ __device__ __forceinline__ uint32_t unblock(const BlockMap &q, uint32_t e) {
     return (gy * q.fh + fy) * q.wd + gx * q.fw + fx;
 }
 
-template <int LAYOUT, int TMW, int KS, bool FUSED, bool LN, bool XM = false>
+template <int LAYOUT, int TMW, int KS, bool FUSED, bool LN, bool XM = false, bool XMUL = false>
 __device__ void body(const GemmArgs &a) {
     constexpr int TW = 16 * TMW;    // weight outputs per tile
     constexpr int NACC = 16 * TMW;  // accumulator floats per lane
@@ -154,9 +154,17 @@ __device__ void body(const GemmArgs &a) {
         lsc = a.ln.scale + 4 * g + S0 * 16;
         lbi = a.ln.bias + 4 * g + S0 * 16;
     }
-    auto load = [&](int s, float4 *xv, float4 *wv, float4 *lv) {
+    // A folded Mul: X = B * B2 elementwise, B2 read at X's offsets.
+    const float *xq[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) xq[q] = XMUL ? a.B2 + (int64_t)b * a.sB + (xp[q] - X) : nullptr;
+    auto load = [&](int s, float4 *xv, float4 *wv, float4 *lv, float4 *mv) {
 #pragma unroll
         for (int q = 0; q < 4; ++q) xv[q] = ld4(xp[q] + s * xstep);
+        if (XMUL) {
+#pragma unroll
+            for (int q = 0; q < 4; ++q) mv[q] = ld4(xq[q] + s * xstep);
+        }
 #pragma unroll
         for (int mt = 0; mt < TMW; ++mt) wv[mt] = ld4(wp[mt] + s * 16);
         if (LN) {
@@ -174,8 +182,17 @@ __device__ void body(const GemmArgs &a) {
             xv[q].w = (xv[q].w - lmean.w) * lrstd.w * w + c;
         }
     };
-    auto mma = [&](float4 *xv, const float4 *wv, const float4 *lv) {
+    auto mma = [&](float4 *xv, const float4 *wv, const float4 *lv, const float4 *mv) {
         if (LN) norm(xv, lv);
+        if (XMUL) {  // mx_mul's a * b
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                xv[q].x = xv[q].x * mv[q].x;
+                xv[q].y = xv[q].y * mv[q].y;
+                xv[q].z = xv[q].z * mv[q].z;
+                xv[q].w = xv[q].w * mv[q].w;
+            }
+        }
 #pragma unroll
         for (int t = 0; t < 4; ++t)
 #pragma unroll
@@ -197,18 +214,18 @@ __device__ void body(const GemmArgs &a) {
         else bias[mt] = ld4(a.bias + min(w0 + mt * 16 + 4 * g, wout - 4));
     }
 
-    float4 xa[4], wa[TMW], la[2], xb[4], wb[TMW], lb[2];
-    load(0, xa, wa, la);
+    float4 xa[4], wa[TMW], la[2], ma[4], xb[4], wb[TMW], lb[2], mb[4];
+    load(0, xa, wa, la, ma);
     int s = 0;
     for (; s + 2 <= nSw; s += 2) {
-        load(s + 1, xb, wb, lb);
-        mma(xa, wa, la);
+        load(s + 1, xb, wb, lb, mb);
+        mma(xa, wa, la, ma);
         // unconditional (the last one re-reads the final superstep), so the
         // wait before the next multiply counts only the loads it needs
-        load(min(s + 2, nSw - 1), xa, wa, la);
-        mma(xb, wb, lb);
+        load(min(s + 2, nSw - 1), xa, wa, la, ma);
+        mma(xb, wb, lb, mb);
     }
-    if (s < nSw) mma(xa, wa, la);
+    if (s < nSw) mma(xa, wa, la, ma);
 
     __shared__ float red[KS == 1 ? 1 : 4 * NACC * 64];
     const int64_t cbase = (int64_t)b * a.sC;
@@ -325,21 +342,25 @@ __device__ void body(const GemmArgs &a) {
 
 }  // namespace pw
 
-// mx_pw_{ch,rw}<TMW>[_k4][_ln|_xm][_f]: 256 threads; _k4 splits the
+// mx_pw_{ch,rw}<TMW>[_k4][_ln|_xm|_mul][_f]: 256 threads; _k4 splits the
 // reduction over the block's four waves, _ln folds a channel LayerNorm into X
 // (CH only), _xm reads X through a token map (GateMm over an elided forward
-// permutation), _f applies the fused epilogue.
-#define MXK_PW1(LNAME, LAYOUT, TMW, KS, LN, XM, SUF)                                               \
+// permutation), _mul forms X as the product of two tensors (a folded Mul, CH
+// only), _f applies the fused epilogue.
+#define MXK_PW2(LNAME, LAYOUT, TMW, KS, LN, XM, XMUL, SUF)                                         \
     extern "C" __global__ __launch_bounds__(256) void mx_pw_##LNAME##TMW##SUF(GemmArgs a) {        \
-        pw::body<pw::LAYOUT, TMW, KS, false, LN, XM>(a);                                           \
+        pw::body<pw::LAYOUT, TMW, KS, false, LN, XM, XMUL>(a);                                     \
     }                                                                                               \
     extern "C" __global__ __launch_bounds__(256) void mx_pw_##LNAME##TMW##SUF##_f(GemmArgs a) {    \
-        pw::body<pw::LAYOUT, TMW, KS, true, LN, XM>(a);                                            \
+        pw::body<pw::LAYOUT, TMW, KS, true, LN, XM, XMUL>(a);                                      \
     }
+#define MXK_PW1(LNAME, LAYOUT, TMW, KS, LN, XM, SUF) MXK_PW2(LNAME, LAYOUT, TMW, KS, LN, XM, false, SUF)
 #define MXK_PW(LNAME, LAYOUT, TMW)                                                                 \
     MXK_PW1(LNAME, LAYOUT, TMW, 1, false, false, ) MXK_PW1(LNAME, LAYOUT, TMW, 4, false, false, _k4) \
     MXK_PW1(LNAME, LAYOUT, TMW, 1, false, true, _xm) MXK_PW1(LNAME, LAYOUT, TMW, 4, false, true, _k4_xm)
 #define MXK_PW_LN(TMW) MXK_PW1(ch, CH, TMW, 1, true, false, _ln) MXK_PW1(ch, CH, TMW, 4, true, false, _k4_ln)
+#define MXK_PW_MUL(TMW) \
+    MXK_PW2(ch, CH, TMW, 1, false, false, true, _mul) MXK_PW2(ch, CH, TMW, 4, false, false, true, _k4_mul)
 MXK_PW(ch, CH, 1)
 MXK_PW(ch, CH, 2)
 MXK_PW(ch, CH, 4)
@@ -349,3 +370,6 @@ MXK_PW(rw, RW, 4)
 MXK_PW_LN(1)
 MXK_PW_LN(2)
 MXK_PW_LN(4)
+MXK_PW_MUL(1)
+MXK_PW_MUL(2)
+MXK_PW_MUL(4)

@@ -312,3 +312,42 @@ def test_forward_permutation_elided(gpu_ok, kind, gh, gw, fh, fw):
     gpu.close()
     assert np.array_equal(got.view(np.uint32), plain.view(np.uint32)), "fused and unfused passes differ"
     check(got, oracle_plan(cp, inputs, out), "%s perm elided %dx%d cells of %dx%d" % (kind, gh, gw, fh, fw))
+
+
+@pytest.mark.parametrize("ci,co,h,w,add", [
+    (32, 32, 16, 20, True),     # the cross-gating shape class: Mul -> conv1x1 + residual
+    (128, 128, 7, 12, False),   # K 128: split reduction, 84 pixels (ragged tile)
+    (64, 48, 5, 8, True),
+])
+def test_mul_folded_into_the_dense(gpu_ok, ci, co, h, w, add):
+    """Mul -> Conv1x1 [-> Add] as one streaming launch that multiplies the two
+    factors on the way into the GEMM: the CPU path's result to the GEMM bar,
+    and bitwise the unfused pass."""
+    from maxim_amd import plan as P
+    from maxim_amd import hip as H
+    rng = np.random.default_rng(ci + co + h + w)
+    n = ci * h * w
+    A, B, M_, T, R, Y = range(6)
+    bufs = [(ci, h, w), (ci, h, w), (ci, h, w), (co, h, w), (co, h, w), (co, h, w)]
+    ops = [P.make_op(P.MUL, dst=M_, src=A, src2=B, n=n),
+           P.make_op(P.CONV1X1, dst=T, src=M_, w=0, bias=1, c_in=ci, c_out=co, h=h, wd=w)]
+    if add:
+        ops.append(P.make_op(P.ADD, dst=Y, src=T, src2=R, n=co * h * w))
+    out = Y if add else T
+    wt = he(rng, (co, ci), ci)
+    b = (rng.standard_normal(co) * 0.1).astype(np.float32)
+    cp = P.CustomPlan(bufs, ops, [wt, b], input=A, output=out)
+    inputs = {A: rng.standard_normal(bufs[A]).astype(np.float32), B: rng.standard_normal(bufs[B]).astype(np.float32),
+              R: rng.standard_normal(bufs[R]).astype(np.float32)}
+    got, steps = run_plan(cp, inputs, out)
+    print("steps", steps)
+    assert len(steps) == 1 and "_mul" in steps[0][2], steps
+    gpu = H.Gpu(cp)
+    for k, v in inputs.items():
+        gpu.write_buf(k, v)
+    gpu.set_fusion(False)
+    gpu.run_ops(0, len(cp.ops))
+    plain = gpu.read_buf(out).reshape(got.shape)
+    gpu.close()
+    assert np.array_equal(got.view(np.uint32), plain.view(np.uint32)), "fused and unfused passes differ"
+    check(got, oracle_plan(cp, inputs, out), "mul -> conv1x1 %d->%d @%dx%d%s" % (ci, co, h, w, " + add" if add else ""))
