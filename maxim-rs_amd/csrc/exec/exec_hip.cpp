@@ -151,11 +151,12 @@ std::pair<int64_t, std::string> ln_tile(int64_t c, int64_t hw, int cus) {
 // 128-bit kernel's stride), about 64 per channel, at least 2048 elements.
 int64_t mean_chunk(int64_t hw) { return std::max<int64_t>(2048, ((hw + 63) / 64 + 1023) / 1024 * 1024); }
 
-// The one-pass resize stages, per block of `rows` output rows, the input rows
-// from the first row's first vertical tap to the last row's last one. Returns
-// the most any block needs, or -1 if some row of a block reaches outside that
-// range (taps not monotone), in which case the two-pass kernels run.
-constexpr int kResizeRowsMax = 96, kResizeTapsMax = 8;
+// The one-pass resize stages, per band of `rows` outputs of one axis, the
+// inputs from the first output's first tap to the last output's last one.
+// Returns the most any band needs, or -1 if some output of a band reaches
+// outside that range (taps not monotone), in which case the two-pass kernels
+// run. Used for output rows and for output columns alike.
+constexpr int kResizeLdsMax = 64 * 1024, kResizeTapsMax = 8;
 int resize_band(const std::vector<float> &tv, int mt, int64_t n_out, int64_t rows) {
     const size_t sv = 3 + (size_t)mt;
     int most = 0;
@@ -1057,34 +1058,43 @@ void Gpu::build_launches(const mx_plan_desc *p, const std::vector<int64_t> &woff
             }
             case MX_OP_RESIZE: {
                 // One pass when the taps of both axes are at most 8 and a
-                // band of output rows reads few enough input rows: the most
-                // rows per block that still leaves >= 2048 blocks, else the
-                // band with the most blocks.
-                if (maxt[i][0] <= kResizeTapsMax && !std::getenv("MAXIM_RESIZE_2PASS")) {
-                    int mv = 0;
+                // block's input rows and columns fit its LDS: 256 output
+                // columns per block (128-bit stores) unless the columns are
+                // downsampled, then 64; the most output rows per block that
+                // still leaves >= 2048 blocks, else the band with the most.
+                if (maxt[i][0] <= kResizeTapsMax && maxt[i][1] <= kResizeTapsMax && !std::getenv("MAXIM_RESIZE_2PASS")) {
+                    int mv = 0, mh = 0;
                     const std::vector<float> tv = resize_table(o.h, o.oh, mv);
-                    const int64_t tiles_x = cdiv(o.ow, 64);
-                    int64_t pick = 0;
-                    int pick_band = 0;
-                    for (int64_t rows : {64, 32, 16, 8, 4, 2, 1}) {
-                        const int band = resize_band(tv, mv, o.oh, rows);
-                        if (band < 0 || band > kResizeRowsMax) continue;
-                        pick = rows;
-                        pick_band = band;
-                        if (tiles_x * cdiv(o.oh, rows) * o.c >= 2048) break;
-                    }
-                    if (pick > 0 && mv <= kResizeTapsMax) {
+                    const std::vector<float> th = resize_table(o.wd, o.ow, mh);
+                    bool done = false;
+                    for (int tw : {256, 64}) {
+                        if (tw == 256 && (o.ow < o.wd || o.ow % 4 || !aligned(B(o.dst), 16))) continue;
+                        const int span = resize_band(th, mh, o.ow, tw);
+                        if (span < 0) continue;
+                        const int64_t tiles_x = cdiv(o.ow, tw);
+                        int64_t pick = 0;
+                        int pick_band = 0;
+                        for (int64_t rows : {64, 32, 16, 8, 4, 2, 1}) {
+                            const int band = resize_band(tv, mv, o.oh, rows);
+                            if (band < 0 || 4 * (band * (span + tw) + rows * (3 + mv)) > kResizeLdsMax) continue;
+                            pick = rows;
+                            pick_band = band;
+                            if (tiles_x * cdiv(o.oh, rows) * o.c >= 2048) break;
+                        }
+                        if (pick == 0) continue;
                         Resize2Args r{B(o.src), B(o.dst), X(i, 0), X(i, 1), (int32_t)o.h, (int32_t)o.wd,
                                       (int32_t)o.oh, (int32_t)o.ow, maxt[i][0], maxt[i][1], (int32_t)pick,
-                                      (int32_t)tiles_x, pick_band, 0};
-                        Launch l = mk("mx_resize_hv");
+                                      (int32_t)tiles_x, pick_band, span};
+                        Launch l = mk(tw == 256 ? "mx_resize_hv4" : "mx_resize_hv");
                         l.g[0] = (uint32_t)(tiles_x * cdiv(o.oh, pick));
                         l.g[1] = (uint32_t)o.c;
-                        l.shm = (unsigned)(4 * (pick_band * 64 + pick * (3 + mv)));
+                        l.shm = (unsigned)(4 * (pick_band * (span + tw) + pick * (3 + mv)));
                         set_args(l, r);
                         L.push_back(l);
+                        done = true;
                         break;
                     }
+                    if (done) break;
                 }
                 ResizeArgs h{};
                 h.x = B(o.src);

@@ -93,8 +93,8 @@ struct ResizeArgs {
     int32_t n_in, n_out, width, axis;
 };
 
-// Both resize axes in one pass (mx_resize_hv): tap tables as for the
-// two-pass kernels, `rows` output rows x 64 output columns per block.
+// Both resize axes in one pass (mx_resize_hv[4]): tap tables as for the
+// two-pass kernels, `rows` output rows x 64 (256) output columns per block.
 struct Resize2Args {
     const float *x;
     float *y;
@@ -102,7 +102,7 @@ struct Resize2Args {
     int32_t h, wd, oh, ow;  // input and output plane
     int32_t mth, mtv;       // taps per table row
     int32_t rows, tiles_x;  // output rows per block, column tiles per row band
-    int32_t band, pad;      // LDS rows of horizontal results (the most any block needs)
+    int32_t band, span;     // LDS input rows and columns (the most any block reads)
 };
 
 // Nearest subsample.

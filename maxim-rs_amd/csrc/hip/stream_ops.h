@@ -487,72 +487,122 @@ extern "C" __global__ __launch_bounds__(MXK_BLOCK) void mx_resize_v(ResizeArgs a
     a.y[i] = ws > 0.0f ? acc / ws : acc;
 }
 
-// Both axes in one pass, without the intermediate plane. A block owns 64
-// output columns x `rows` output rows of one channel: it first runs the
-// horizontal pass for the input rows those outputs read (the vertical taps of
-// its first row through those of its last, at most `band` rows, which the host
-// sizes the dynamic LDS for) into LDS, with the band's vertical taps beside
-// them, then the vertical pass from LDS to the output. Every intermediate value
-// is computed by the same expression as in mx_resize_h, so the result is
-// bit-identical to the two-pass kernels; rows shared by two blocks are simply
-// computed twice. Both tables are at most RS_MAXT taps wide (checked by the
-// host); the horizontal taps of a lane's column live in registers.
-constexpr int RS_TW = 64;
+// Both axes in one pass, without the intermediate plane. A block owns TW
+// output columns x `rows` output rows of one channel. It stages in LDS the
+// input rows its outputs read (the vertical taps of its first row through
+// those of its last: `band` rows at most) over the input columns they read
+// (the horizontal taps of its first column through those of its last: `span`
+// at most; the host sizes the dynamic LDS and checks both ranges), with
+// coalesced loads; runs the horizontal pass from there into LDS; and then the
+// vertical pass from LDS to the output. Every intermediate value is computed
+// by the same expression as in mx_resize_h, so the result is bit-identical to
+// the two-pass kernels; rows and columns shared by two blocks are simply
+// staged twice. Tables are at most RS_MAXT taps wide (checked by the host).
+// TW = 64: one output column per lane; TW = 256 (ow % 4 == 0, 16-byte aligned
+// y): four adjacent columns per lane in the vertical pass, 128-bit stores.
 constexpr int RS_MAXT = 8;
 
-extern "C" __global__ __launch_bounds__(256) void mx_resize_hv(Resize2Args a) {
+// acc / wsum when wsum > 0 (the CPU path's normalisation). Upsampling tables
+// mostly sum to exactly 1, and x / 1 is x in IEEE arithmetic, so those skip
+// the division and the result is the same to the bit.
+__device__ __forceinline__ float rs_norm(float acc, float ws) {
+    return ws > 0.0f && ws != 1.0f ? acc / ws : acc;
+}
+
+template <int TW>
+__device__ void resize_hv(const Resize2Args &a) {
     extern __shared__ float rs_lds[];
-    float *tmp = rs_lds;                     // [band][64]
-    float *vt = rs_lds + a.band * RS_TW;     // [rows][3 + mtv]
-    const int lane = threadIdx.x & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    float *in = rs_lds;                               // [band][span]
+    float *tmp = rs_lds + a.band * a.span;            // [band][TW]
+    float *vt = tmp + a.band * TW;                    // [rows][3 + mtv]
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int ch = blockIdx.y;
     const int tx = blockIdx.x % a.tiles_x, ty = blockIdx.x / a.tiles_x;
-    const int ox0 = tx * RS_TW, oy0 = ty * a.rows;
-    const int nrow = min(a.rows, a.oh - oy0);
+    const int ox0 = tx * TW, oy0 = ty * a.rows;
+    const int nrow = min(a.rows, a.oh - oy0), ncol = min(TW, a.ow - ox0);
     const int sv = 3 + a.mtv, sh = 3 + a.mth;
     const float *vf = a.tv + (int64_t)oy0 * sv, *vl = vf + (int64_t)(nrow - 1) * sv;
-    const int jlo = (int)vf[0];
-    const int nr = (int)vl[0] + (int)vl[1] - jlo;
-    for (int q = threadIdx.x; q < nrow * sv; q += 256) vt[q] = vf[q];
-
-    const int ox = ox0 + lane;
-    const bool col = ox < a.ow;
-    int j0 = 0, nt = 0;
-    float ws = 0.0f, w[RS_MAXT];
-    if (col) {
-        const float *e = a.th + (int64_t)ox * sh;
-        j0 = (int)e[0];
-        nt = (int)e[1];
-        ws = e[2];
+    const float *hf = a.th + (int64_t)ox0 * sh, *hl = hf + (int64_t)(ncol - 1) * sh;
+    const int jlo = (int)vf[0], nr = (int)vl[0] + (int)vl[1] - jlo;
+    const int xlo = (int)hf[0], xn = (int)hl[0] + (int)hl[1] - xlo;
+    for (int q = tid; q < nrow * sv; q += 256) vt[q] = vf[q];
+    const float *src = a.x + ((int64_t)ch * a.h + jlo) * a.wd + xlo;
+    for (int q = tid; q < nr * xn; q += 256) {
+        const int r = q / xn, c = q - r * xn;
+        in[r * a.span + c] = src[(int64_t)r * a.wd + c];
     }
+    __syncthreads();
+
+    // horizontal pass: TW = 256, thread t owns column t over every row;
+    // TW = 64, lane l owns column l over the rows of its wave
+    const int col = TW == 256 ? tid : lane;
+    if (col < ncol) {
+        const float *e = a.th + (int64_t)(ox0 + col) * sh;
+        const int b = (int)e[0] - xlo, nt = (int)e[1];
+        const float ws = e[2];
+        float w[RS_MAXT];
 #pragma unroll
-    for (int k = 0; k < RS_MAXT; ++k) w[k] = (col && k < a.mth) ? a.th[(int64_t)ox * sh + 3 + k] : 0.0f;
-    const float *xs = a.x + (int64_t)ch * a.h * a.wd + j0 + (int64_t)jlo * a.wd;
-    if (col) {
-#pragma unroll 2
-        for (int r = wave; r < nr; r += 4) {
-            const float *s = xs + (int64_t)r * a.wd;
+        for (int k = 0; k < RS_MAXT; ++k) w[k] = k < a.mth ? e[3 + k] : 0.0f;
+        const int r0 = TW == 256 ? 0 : wave, dr = TW == 256 ? 1 : 4;
+        for (int r = r0; r < nr; r += dr) {
+            const float *sr = in + r * a.span + b;
             float acc = 0.0f;
 #pragma unroll
             for (int k = 0; k < RS_MAXT; ++k)
-                if (k < nt) acc += w[k] * s[k];
-            tmp[r * RS_TW + lane] = ws > 0.0f ? acc / ws : acc;
+                if (k < nt) acc += w[k] * sr[k];
+            tmp[r * TW + col] = rs_norm(acc, ws);
         }
     }
     __syncthreads();
-    if (!col) return;
-    float *yc = a.y + ((int64_t)ch * a.oh + oy0) * a.ow + ox;
-#pragma unroll 2
-    for (int r = wave; r < nrow; r += 4) {
-        const float *e = vt + r * sv;
-        const int b = (int)e[0] - jlo, n = (int)e[1];
-        const float vs = e[2];
-        const float *t = tmp + b * RS_TW + lane;
-        float acc = 0.0f;
+
+    // vertical pass, wave w takes output rows w, w + 4, ...
+    float *yrow = a.y + ((int64_t)ch * a.oh + oy0) * a.ow + ox0;
+    if (TW == 256) {
+        const int c0 = 4 * lane;
+        if (c0 >= ncol) return;
+        for (int r = wave; r < nrow; r += 4) {
+            const float *e = vt + r * sv;
+            const int b = (int)e[0] - jlo, n = (int)e[1];
+            const float vs = e[2];
+            float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-        for (int k = 0; k < RS_MAXT; ++k)
-            if (k < n) acc += e[3 + k] * t[k * RS_TW];
-        yc[(int64_t)r * a.ow] = vs > 0.0f ? acc / vs : acc;
+            for (int k = 0; k < RS_MAXT; ++k)
+                if (k < n) {
+                    const float wk = e[3 + k];
+                    const float4 t = ld4(tmp + (b + k) * TW + c0);
+                    acc[0] += wk * t.x;
+                    acc[1] += wk * t.y;
+                    acc[2] += wk * t.z;
+                    acc[3] += wk * t.w;
+                }
+            float o[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) o[u] = rs_norm(acc[u], vs);
+            float *yo = yrow + (int64_t)r * a.ow + c0;
+            if (c0 + 3 < ncol) {
+                st4(yo, make_float4(o[0], o[1], o[2], o[3]));
+            } else {
+#pragma unroll
+                for (int u = 0; u < 4; ++u)
+                    if (c0 + u < ncol) yo[u] = o[u];
+            }
+        }
+    } else {
+        if (lane >= ncol) return;
+        for (int r = wave; r < nrow; r += 4) {
+            const float *e = vt + r * sv;
+            const int b = (int)e[0] - jlo, n = (int)e[1];
+            const float vs = e[2];
+            const float *t = tmp + b * TW + lane;
+            float acc = 0.0f;
+#pragma unroll
+            for (int k = 0; k < RS_MAXT; ++k)
+                if (k < n) acc += e[3 + k] * t[k * TW];
+            yrow[(int64_t)r * a.ow + lane] = rs_norm(acc, vs);
+        }
     }
 }
+
+extern "C" __global__ __launch_bounds__(256) void mx_resize_hv(Resize2Args a) { resize_hv<64>(a); }
+extern "C" __global__ __launch_bounds__(256) void mx_resize_hv4(Resize2Args a) { resize_hv<256>(a); }

@@ -2,10 +2,11 @@
 
 The resize op (src/exec_cpu.rs:1195-1260) runs a horizontal then a vertical
 pass of tap sums. The executor runs both in one kernel when the taps allow
-(mx_resize_hv: the horizontal rows a band of outputs needs are rebuilt in LDS)
-and as two kernels through the intermediate plane otherwise; both must match
-the CPU path exactly, including at ragged widths, odd ratios and the
-MAXIM pyramid's x4 / x2 / /2 / /4 steps.
+(mx_resize_hv / _hv4: a block stages the input rows and columns its outputs
+read in LDS and rebuilds the horizontal rows there; 64 or 256 output columns
+per block) and as two kernels through the intermediate plane otherwise; all
+must match the CPU path exactly, including at ragged widths, odd ratios,
+partial tiles and the MAXIM pyramid's x4 / x2 / /2 / /4 steps.
 """
 
 import os
@@ -26,6 +27,8 @@ CASES = [
     (5, 64, 64, 64, 64),      # identity
     (1, 1, 1, 3, 130),        # one input pixel
     (2, 9, 130, 9, 65),       # one axis only
+    (2, 30, 70, 60, 300),     # 256-column tiles, the second one partial
+    (3, 13, 57, 40, 172),     # odd upsampling ratios, 256-column tiles
 ]
 
 
@@ -64,7 +67,9 @@ def test_resize_bit_exact(gpu_ok, c, h, w, oh, ow, two_pass):
     if two_pass:
         assert kernels == ["mx_resize_h", "mx_resize_v"], kernels
     else:
-        assert kernels == ["mx_resize_hv"], kernels
+        # 256-column tiles where the columns are not downsampled and ow % 4 == 0
+        kern = "mx_resize_hv4" if ow >= w and ow % 4 == 0 else "mx_resize_hv"
+        assert kernels == [kern], kernels
     assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), \
         float(np.abs(got.astype(np.float64) - want).max())
 
@@ -78,6 +83,6 @@ def test_resize_pyramid_shapes(gpu_ok):
         print("resize %dx%dx%d -> %dx%d" % (c, h, w, oh, ow), flush=True)
         x = rng.standard_normal((c, h, w)).astype(np.float32)
         got, kernels = run_resize(c, h, w, oh, ow, x, False)
-        assert kernels == ["mx_resize_hv"], kernels
+        assert kernels == ["mx_resize_hv4" if ow > w else "mx_resize_hv"], kernels
         want = O.resize(x, oh, ow)
         assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
