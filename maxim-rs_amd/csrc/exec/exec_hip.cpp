@@ -702,6 +702,12 @@ Gpu::Gpu(const mx_plan_desc *p) : H(hip()), doff(pg.doff) {
                     for (int64_t m = 0; m < o.c_out; ++m)
                         for (int tp = 0; tp < 4; ++tp) t[(tp * o.c_out + m) * o.c_in + c] = w[(c * o.c_out + m) * 4 + tp];
                 extra[i][0] = placev(t);
+                // and rows ordered (ky, oc, kx) for the streaming kernels' _t form
+                for (int64_t c = 0; c < o.c_in; ++c)
+                    for (int64_t m = 0; m < o.c_out; ++m)
+                        for (int tp = 0; tp < 4; ++tp)
+                            t[(((tp >> 1) * o.c_out + m) * 2 + (tp & 1)) * o.c_in + c] = w[(c * o.c_out + m) * 4 + tp];
+                extra[i][1] = placev(t);
                 as_is(o.bias);
                 break;
             }
@@ -961,6 +967,19 @@ void Gpu::build_launches(const mx_plan_desc *p, const std::vector<int64_t> &woff
                 a.epi = MXK_EPI_CONVT;
                 a.co = (int32_t)o.c_out;
                 a.wd = (int32_t)o.wd;
+                if (o.wd % 4 == 0) {
+                    // the streaming kernels: each lane pair stores eight
+                    // contiguous outputs of one output row
+                    GemmArgs pa = a;
+                    pa.A = X(i, 1);
+                    Launch pl;
+                    if (try_pw(0, pa, pl)) {
+                        pl.name = intern(std::string(pl.name) + "_t");
+                        pl.f = fn(pl.name);
+                        L.push_back(pl);
+                        break;
+                    }
+                }
                 Tile t = pick_tile(a.M, plane, 1, cus);
                 Launch l = mk(gemm_name(t, o.c_in % 4 == 0 && aligned(a.A, 16)) + "_t");
                 l.g[0] = cdiv(plane, t.bn);

@@ -60,7 +60,7 @@ __device__ __forceinline__ uint32_t unblock(const BlockMap &q, uint32_t e) {
     return (gy * q.fh + fy) * q.wd + gx * q.fw + fx;
 }
 
-template <int LAYOUT, int TMW, int KS, bool FUSED, bool LN, bool XM = false, bool XMUL = false>
+template <int LAYOUT, int TMW, int KS, bool FUSED, bool LN, bool XM = false, bool XMUL = false, bool CT = false>
 __device__ void body(const GemmArgs &a) {
     constexpr int TW = 16 * TMW;    // weight outputs per tile
     constexpr int NACC = 16 * TMW;  // accumulator floats per lane
@@ -210,7 +210,10 @@ __device__ void body(const GemmArgs &a) {
 #pragma unroll
     for (int mt = 0; mt < TMW; ++mt) {
         if (!a.bias) continue;
-        if (LAYOUT == CH) bias[mt].x = a.bias[min(w0 + mt * 16 + i, wout - 1)];
+        if (LAYOUT == CH) {
+            const int m = min(w0 + mt * 16 + i, wout - 1);
+            bias[mt].x = a.bias[CT ? (m % (2 * a.co)) >> 1 : m];  // CT: row (ky, oc, kx) has oc's bias
+        }
         else bias[mt] = ld4(a.bias + min(w0 + mt * 16 + 4 * g, wout - 4));
     }
 
@@ -279,7 +282,8 @@ __device__ void body(const GemmArgs &a) {
         if (FUSED && k + 1 < NK) operands(k + 1, (k + 1) & 1);
         const int mt = KS == 1 ? k / 4 : k, x = KS == 1 ? k % 4 : wave;
         int64_t off;
-        if (!where(k, off)) continue;
+        const bool inside = where(k, off);
+        if (!CT && !inside) continue;  // CT: both lanes of a pair share this, and both shuffle
         float v[4];
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
@@ -336,6 +340,22 @@ __device__ void body(const GemmArgs &a) {
                 v[3] = v[3] + o2[bi].w;
             }
         }
+        if (CT) {
+            // Transposed 2x2 stride-2 conv: row m = (ky * co + oc) * 2 + kx, so
+            // lanes i and i ^ 1 hold kx = 0 and 1 of one (ky, oc) for the same
+            // four input pixels (x .. x + 3 of input row y): together the eight
+            // contiguous outputs 2x .. 2x + 7 of output row 2y + ky, four each.
+            float pv[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) pv[u] = __shfl_xor(v[u], 1);
+            if (!inside) continue;
+            const int m = w0 + mt * 16 + i, two = 2 * a.co;
+            const int ky = m / two, rem = m - ky * two, oc = rem >> 1, kx = rem & 1;
+            const int n = (int)(off - (int64_t)m * N), y = n / a.wd, xx = n - y * a.wd;
+            float *o = Y + (int64_t)oc * 4 * N + (int64_t)(2 * y + ky) * (2 * a.wd) + 2 * xx + 4 * kx;
+            st4(o, kx == 0 ? make_float4(v[0], pv[0], v[1], pv[1]) : make_float4(pv[2], v[2], pv[3], v[3]));
+            continue;
+        }
         st4(Y + placed(off), make_float4(v[0], v[1], v[2], v[3]));
     }
 }
@@ -346,7 +366,9 @@ __device__ void body(const GemmArgs &a) {
 // reduction over the block's four waves, _ln folds a channel LayerNorm into X
 // (CH only), _xm reads X through a token map (GateMm over an elided forward
 // permutation), _mul forms X as the product of two tensors (a folded Mul, CH
-// only), _f applies the fused epilogue.
+// only), _f applies the fused epilogue. mx_pw_ch<TMW>[_k4]_t: the transposed
+// 2x2 stride-2 conv (rows ordered (ky, oc, kx), co and the input width in
+// GemmArgs co / wd, wd % 4 == 0).
 #define MXK_PW2(LNAME, LAYOUT, TMW, KS, LN, XM, XMUL, SUF)                                         \
     extern "C" __global__ __launch_bounds__(256) void mx_pw_##LNAME##TMW##SUF(GemmArgs a) {        \
         pw::body<pw::LAYOUT, TMW, KS, false, LN, XM, XMUL>(a);                                     \
@@ -359,6 +381,10 @@ __device__ void body(const GemmArgs &a) {
     MXK_PW1(LNAME, LAYOUT, TMW, 1, false, false, ) MXK_PW1(LNAME, LAYOUT, TMW, 4, false, false, _k4) \
     MXK_PW1(LNAME, LAYOUT, TMW, 1, false, true, _xm) MXK_PW1(LNAME, LAYOUT, TMW, 4, false, true, _k4_xm)
 #define MXK_PW_LN(TMW) MXK_PW1(ch, CH, TMW, 1, true, false, _ln) MXK_PW1(ch, CH, TMW, 4, true, false, _k4_ln)
+#define MXK_PW_CT(TMW, KS, SUF)                                                                    \
+    extern "C" __global__ __launch_bounds__(256) void mx_pw_ch##TMW##SUF##_t(GemmArgs a) {          \
+        pw::body<pw::CH, TMW, KS, false, false, false, false, true>(a);                             \
+    }
 #define MXK_PW_MUL(TMW) \
     MXK_PW2(ch, CH, TMW, 1, false, false, true, _mul) MXK_PW2(ch, CH, TMW, 4, false, false, true, _k4_mul)
 MXK_PW(ch, CH, 1)
@@ -373,3 +399,9 @@ MXK_PW_LN(4)
 MXK_PW_MUL(1)
 MXK_PW_MUL(2)
 MXK_PW_MUL(4)
+MXK_PW_CT(1, 1, )
+MXK_PW_CT(1, 4, _k4)
+MXK_PW_CT(2, 1, )
+MXK_PW_CT(2, 4, _k4)
+MXK_PW_CT(4, 1, )
+MXK_PW_CT(4, 4, _k4)

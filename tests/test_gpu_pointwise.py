@@ -351,3 +351,29 @@ def test_mul_folded_into_the_dense(gpu_ok, ci, co, h, w, add):
     gpu.close()
     assert np.array_equal(got.view(np.uint32), plain.view(np.uint32)), "fused and unfused passes differ"
     check(got, oracle_plan(cp, inputs, out), "mul -> conv1x1 %d->%d @%dx%d%s" % (ci, co, h, w, " + add" if add else ""))
+
+
+@pytest.mark.parametrize("ci,co,h,w", [
+    (128, 64, 12, 20),   # streaming _t form, split reduction
+    (64, 32, 7, 8),      # 56 pixels: one partial tile
+    (32, 48, 4, 12),     # 192 rows (ky, oc, kx): a partial weight block
+    (32, 16, 5, 6),      # width not a multiple of 4: the tiled GEMM's scatter
+    (24, 8, 4, 8),       # K 24: the tiled GEMM
+])
+def test_transposed_conv_edges(gpu_ok, ci, co, h, w):
+    """ConvT 2x2 stride 2 (src/exec_cpu.rs:846-914) on the streaming kernels
+    (row order (ky, oc, kx), each lane pair storing eight contiguous outputs)
+    and on the tiled fallback, against the CPU path."""
+    from maxim_amd import plan as P
+    from oracle import oracle as O
+    rng = np.random.default_rng(ci * 7 + co + h * w)
+    x = rng.standard_normal((ci, h, w)).astype(np.float32)
+    wt = he(rng, (ci, co, 2, 2), ci)
+    b = (rng.standard_normal(co) * 0.1).astype(np.float32)
+    op = P.make_op(P.CONVT2X2, dst=1, src=0, w=0, bias=1, c_in=ci, c_out=co, h=h, wd=w)
+    cp = P.CustomPlan([(ci, h, w), (co, 2 * h, 2 * w)], [op], [wt, b], input=0, output=1)
+    got, steps = run_plan(cp, {0: x}, 1)
+    print("steps", steps)
+    streaming = w % 4 == 0 and ci % 16 == 0
+    assert steps[0][2].startswith("mx_pw_ch" if streaming else "mx_gemm_") and steps[0][2].endswith("_t"), steps
+    check(got, O.convt2x2(x, wt, b), "convt %d->%d @%dx%d" % (ci, co, h, w))
