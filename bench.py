@@ -223,8 +223,31 @@ def launch_costs(plan, steps, launches, R):
     a folded LayerNorm's statistics pass (reads x, writes mean and 1/std) and
     the GEMM that re-reads x with them, the two resize passes through `tmp`,
     the channel mean's partial and final sums, and the partial sums before
-    the CALayer block that finishes the means."""
+    the CALayer block that finishes the means. A GEMM step that ends in the
+    LayerNorm of an output band (the _lo kernels) is the GEMM step's cost plus
+    the LayerNorm's output, less the band's raw store when nothing else
+    reads it."""
+    from maxim_amd import plan as P
+
+    def read_later(buf, after):
+        """Whether an op after `after` reads buf's bytes before they are rewritten."""
+        lo, hi = int(plan.offs[buf]), int(plan.offs[buf]) + plan.buf_len(buf)
+        for k in range(after + 1, len(plan.ops)):
+            o = plan.ops[k]
+            for s in plan.operands(o)[1:]:
+                if s >= 0 and int(plan.offs[s]) < hi and lo < int(plan.offs[s]) + plan.buf_len(s):
+                    return True
+            d = o.dst
+            if int(plan.offs[d]) <= lo and hi <= int(plan.offs[d]) + plan.buf_len(d):
+                return False
+        return False
+
     def step_cost(a, b):
+        ln = plan.ops[b - 1]
+        if b - a > 1 and ln.kind == P.CHAN_LN and plan.ops[b - 2].kind != P.CHAN_LN:
+            f, by = step_cost(a, b - 1)
+            band = 4 * ln.c * ln.hw
+            return f, by + band - (0 if read_later(ln.src, b - 1) else band)
         f = sum(R.op_cost(plan.ops[k])[0] for k in range(a, b))
         by = sum(R.op_cost(plan.ops[k])[1] for k in range(a, b))
         by -= sum(8 * plan.buf_len(plan.ops[k].dst) for k in range(a, b - 1))
@@ -248,7 +271,8 @@ def launch_costs(plan, steps, launches, R):
                 f, by = step_cost(a, b)
                 out[i] = (f, by + 8 * o.hw)  # + the statistics it reads
             elif kn.startswith("mx_chan_ln"):  # a LayerNorm that could not be folded
-                out[i] = R.op_cost(o)
+                last = plan.ops[b - 1]
+                out[i] = R.op_cost(last if b - 1 > a and last.kind == P.CHAN_LN else o)
             elif kn == "mx_resize_h":
                 out[i] = (0, 4 * (o.c * o.h * o.wd + o.c * o.h * o.ow))
             elif kn == "mx_resize_v":

@@ -40,7 +40,7 @@ struct Launch {
     unsigned g[3] = {1, 1, 1};
     unsigned b[3] = {MXK_BLOCK, 1, 1};
     unsigned shm = 0;  // dynamic LDS bytes
-    alignas(16) unsigned char a0[256];
+    alignas(16) unsigned char a0[320];
     alignas(16) unsigned char a1[32];
     int nparams = 1;
     int kind = 0;  // 1: a0 holds GemmArgs (plain epilogue), 2: ConvArgs
@@ -276,6 +276,11 @@ struct StepSpec {
     // (r1p: the permutation's output, read instead if a kernel cannot map).
     int64_t xperm = -1, xsrc = -1, rperm = -1, r1p = -1;
     int64_t xmul = -1;  // a Mul folded into the next op's GEMM operand (== first)
+    // A LayerNorm of (a band of) the GEMM's output, op lno == last - 1,
+    // computed in the streaming kernel's epilogue (_lo); lno_keep: the raw
+    // band is read elsewhere too, so it is still stored.
+    int64_t lno = -1;
+    bool lno_keep = true;
 };
 
 struct Program {
@@ -1553,6 +1558,45 @@ void Program::plan_fusion(const mx_plan_desc *p, bool require_clear) {
         K.r1 = S;
         ++fused_ops;
     }
+
+    // LayerNorm of a 1x1 conv's output band in the conv's epilogue: a
+    // stand-alone ChanLn of 32, 64 or 128 channels whose input is a whole
+    // band of channels of the GEMM step just before it (the gMLP gate's v
+    // half after its in-projection, the RCAB's input after an out-projection
+    // + residual). One wave, or a few waves of one block, of the streaming
+    // kernel hold every channel of the band for their pixels, so they
+    // normalise them there; the LayerNorm's step joins the GEMM's.
+    std::vector<StepSpec> merged;
+    const bool lno_on = !std::getenv("MAXIM_NO_LN_EPILOGUE");
+    for (uint64_t s = 0; s < specs.size(); ++s) {
+        StepSpec sp = specs[s];
+        if (lno_on && s + 1 < specs.size() && sp.rule == RULE_NONE && sp.perm < 0 && sp.xmul < 0 && sp.lno < 0) {
+            const StepSpec &L = specs[s + 1];
+            const uint64_t g = sp.ln >= 0 ? sp.first + 1 : sp.first;
+            const mx_op &c = p->ops[g], &ln = p->ops[L.first];
+            const int64_t y = sp.out >= 0 ? sp.out : c.dst, hw = c.h * c.wd;
+            const R yr = range(y), lr = range(ln.src);
+            if (L.first == sp.last && L.last == L.first + 1 && L.rule == RULE_NONE && ln.kind == MX_OP_CHAN_LN &&
+                c.kind == MX_OP_CONV1X1 && hw > 1 && ln.hw == hw && (ln.c == 32 || ln.c == 64 || ln.c == 128) &&
+                lr.a >= yr.a && lr.b <= yr.b && (lr.a - yr.a) % (uint64_t)hw == 0 &&
+                ((lr.a - yr.a) / (uint64_t)hw) % (uint64_t)ln.c == 0) {
+                std::vector<int64_t> reads = reads_of(c);
+                if (sp.ln >= 0) reads.push_back(p->ops[sp.ln].src);
+                for (int64_t r : {sp.u, sp.r1, sp.r2, sp.xsrc, y})
+                    if (r >= 0) reads.push_back(r);
+                if (clear_of(ln.dst, reads) && !overlap(range(ln.dst), lr)) {
+                    sp.lno = (int64_t)L.first;
+                    sp.lno_keep = !only_reader(ln.src, L.first - 1, L.first) || (uint64_t)ln.src == p->output ||
+                                  (uint64_t)y == p->output || (p->keep && (p->keep[ln.src] || p->keep[y]));
+                    sp.last = L.last;
+                    ++fused_ops;
+                    ++s;
+                }
+            }
+        }
+        merged.push_back(sp);
+    }
+    specs.swap(merged);
 }
 
 // The device arena: the plan's own packing rule (largest first, first use as
@@ -1762,6 +1806,82 @@ void Gpu::build_program(const mx_plan_desc *p) {
         a.xmap = BlockMap{q.h * q.wd, 1, (int32_t)q.p[2], (int32_t)q.p[3], (int32_t)q.p[1], (int32_t)q.wd, 0};
         set_args(l, a);
     };
+    // A GEMM step that also computes the LayerNorm of an output band (lno):
+    // its streaming kernel's _lo form with a wave-wide band, or, where the
+    // step's kernel cannot take it (not streaming, another operand form, a
+    // misaligned or overlapping LayerNorm output), the LayerNorm's own
+    // launch after the step's.
+    auto lno_apply = [&](const StepSpec &sp, Step &st) {
+        if (sp.lno < 0) return;
+        const mx_op &ln = p->ops[sp.lno];
+        Launch &l = st.launches[st.main];
+        std::string nm = l.name;
+        GemmArgs a;
+        memcpy(&a, l.a0, sizeof a);
+        ChanLnArgs la;
+        memcpy(&la, ops[sp.lno][0].a0, sizeof la);
+        bool ok = !strncmp(l.name, "mx_pw_ch", 8) && l.kind == 1 && a.batch == 1 && !a.ymap.on && a.N == ln.hw &&
+                  aligned(la.y, 16);
+        const bool lnn = nm.find("_ln") != std::string::npos;
+        if (ok) {
+            // the name is mx_pw_ch<T>[_k4][_ln][_f]: nothing else may be folded in
+            std::string rest = nm.substr(9);
+            for (const char *t : {"_k4", "_ln", "_f"})
+                if (!rest.compare(0, strlen(t), t)) rest = rest.substr(strlen(t));
+            ok = rest.empty();
+        }
+        const int64_t row0 = ok ? (la.x - a.C) : -1;
+        ok = ok && row0 >= 0 && row0 % a.N == 0 && (row0 / a.N) % ln.c == 0 && row0 / a.N + ln.c <= a.M;
+        if (ok) {
+            // the LayerNorm's output may overlap nothing the kernel reads or writes
+            const float *lo = la.y, *hi = la.y + ln.c * ln.hw;
+            auto clash = [&](const float *b, int64_t n) { return b && b < hi && lo < b + n; };
+            const int64_t xn = (int64_t)a.K * a.N;
+            ok = !clash(a.C, (int64_t)a.M * a.N) && !clash(a.B, xn) && !clash(a.B2, xn) &&
+                 !clash(a.e.u, (int64_t)a.M * a.N) && !clash(a.e.r1, (int64_t)a.M * a.N) &&
+                 !clash(a.e.r2, (int64_t)a.M * a.N) && !clash(a.A, (int64_t)a.M * a.K);
+            if (ok && a.xmap.on) ok = !clash(a.B, a.xmap.plane * a.K);
+            if (ok && a.ln.mean) ok = !clash(a.ln.mean, 2 * (int64_t)a.N);
+        }
+        if (!ok) {
+            for (const Launch &x : ops[sp.lno]) st.launches.push_back(x);
+            return;
+        }
+        // The tile: the step's own width when G = C / width consecutive
+        // waves of a block hold the band (G = 1 also with the split
+        // reduction; G > 1 needs whole blocks of tiles, groups aligned to
+        // the block), else a width of C itself. The reduction split stays
+        // as the step has it: the tile width does not change any output's
+        // order of accumulation, the split does, and the fused pass stays
+        // the unfused one to the bit.
+        const int r0 = (int)(row0 / a.N);
+        auto fits = [&](int tmw, bool k4) {
+            const int tw = 16 * tmw, G = (int)(ln.c / tw);
+            if (ln.c % tw || (G != 1 && G != 2 && G != 4) || (k4 && G != 1)) return 0;
+            const int64_t nib = (a.M + tw - 1) / tw, tiles = nib * ((a.N + 63) / 64);
+            if (G > 1 && (nib % G || (r0 / tw) % G || tiles % 4)) return 0;
+            return G;
+        };
+        const int tmw0 = nm[8] - '0';
+        const bool k40 = nm.find("_k4") != std::string::npos;
+        const bool k4 = k40;
+        int tmw = tmw0, G = fits(tmw0, k4);
+        if (!G && (ln.c == 32 || ln.c == 64)) {
+            tmw = (int)(ln.c / 16);
+            G = 1;
+        }
+        if (!G) {
+            for (const Launch &x : ops[sp.lno]) st.launches.push_back(x);
+            return;
+        }
+        const int64_t tiles = ((a.M + 16 * tmw - 1) / (16 * tmw)) * ((a.N + 63) / 64);
+        l.name = intern("mx_pw_ch" + std::to_string(tmw) + (k4 ? "_k4" : "") + (lnn ? "_ln" : "") + "_f_lo");
+        l.f = fn(l.name);
+        l.g[0] = (unsigned)(k4 ? tiles : (tiles + 3) / 4);
+        l.g[1] = 1;
+        a.lo = LnOut{la.scale, la.bias, la.y, la.eps, r0, sp.lno_keep ? 1 : 0, G};
+        set_args(l, a);
+    };
     prog.clear();
     for (const StepSpec &sp : pg.specs) {
         if (sp.rule == RULE_ELIDED) {
@@ -1838,7 +1958,9 @@ void Gpu::build_program(const mx_plan_desc *p) {
         if (sp.ln < 0) {
             std::vector<Launch> v = sp.out < 0 ? ops[sp.first] : gemm_part(sp, sp.first);
             if (sp.xperm >= 0) token_map(sp, v[0]);
-            prog.push_back(Step{sp.first, sp.last, v});
+            Step st{sp.first, sp.last, v};
+            lno_apply(sp, st);
+            prog.push_back(st);
             continue;
         }
         // A LayerNorm folded into the next op's streaming GEMM: the
@@ -1862,6 +1984,7 @@ void Gpu::build_program(const mx_plan_desc *p) {
             Step st{sp.first, sp.last, ops[sp.first]};
             st.main = st.launches.size();
             for (const Launch &x : gp) st.launches.push_back(x);
+            lno_apply(sp, st);
             prog.push_back(st);
             continue;
         }
@@ -1895,6 +2018,7 @@ void Gpu::build_program(const mx_plan_desc *p) {
         Step st{sp.first, sp.last, {sl}};
         for (const Launch &x : gp) st.launches.push_back(x);
         st.main = 1;
+        lno_apply(sp, st);
         prog.push_back(st);
     }
 }

@@ -155,6 +155,19 @@ struct BlockMap {
     int32_t on, fh, fw, gw, wd, r1map;
 };
 
+// A channel LayerNorm of a channel-major GEMM's output (the streaming
+// kernels' _lo form, one batch): output rows row0 .. row0 + C - 1, C being
+// the tile width of `group` consecutive waves of a block, are normalised per
+// pixel with the LayerNorm kernels' order and expression and written to y as
+// [C][N]; keep = 0 leaves those rows' raw values unstored (nothing else
+// reads them).
+struct LnOut {
+    const float *scale, *bias;
+    float *y;
+    float eps;
+    int32_t row0, keep, group;
+};
+
 struct GemmArgs {
     const float *A;
     const float *B;
@@ -169,6 +182,7 @@ struct GemmArgs {
     LnIn ln;
     BlockMap ymap, xmap;
     const float *B2;      // _mul: X is B * B2 elementwise (a folded Mul), same layout
+    LnOut lo;
 };
 
 // Small GEMV for the plane-1 CALayer convs: y[o] = b[o] + sum_i w[o][i] x[i].

@@ -60,7 +60,8 @@ __device__ __forceinline__ uint32_t unblock(const BlockMap &q, uint32_t e) {
     return (gy * q.fh + fy) * q.wd + gx * q.fw + fx;
 }
 
-template <int LAYOUT, int TMW, int KS, bool FUSED, bool LN, bool XM = false, bool XMUL = false, bool CT = false>
+template <int LAYOUT, int TMW, int KS, bool FUSED, bool LN, bool XM = false, bool XMUL = false, bool CT = false,
+          bool LNO = false>
 __device__ void body(const GemmArgs &a) {
     constexpr int TW = 16 * TMW;    // weight outputs per tile
     constexpr int NACC = 16 * TMW;  // accumulator floats per lane
@@ -276,9 +277,20 @@ __device__ void body(const GemmArgs &a) {
         if (a.e.r1) o1[buf] = ld4(a.e.r1 + (a.ymap.r1map ? cbase + placed(ok ? off : 0) : at));
         if (a.e.r2) o2[buf] = ld4(a.e.r2 + at);
     };
+    // LNO: the wave whose tile is the output LayerNorm's channels keeps its
+    // final values for it (and stores them raw only when asked to): with
+    // KS = 1 in its own rows of LDS at once, with KS = 4 (where LDS still
+    // holds the partial sums) in registers until every wave has read them.
+    constexpr int PC = KS == 1 ? 64 : 16;  // pixel columns of a wave's tile
+    constexpr int LDT = PC + 4;            // padded LDS row
+    constexpr int PER = TW * LDT + 2 * PC;  // LDS floats per wave
+    __shared__ float lt[LNO && KS == 1 ? 4 * PER : 1];
+    const bool lnw = LNO && w0 >= a.lo.row0 && w0 < a.lo.row0 + (KS == 1 ? a.lo.group : 1) * TW;
+    float4 vs[LNO && KS == 4 ? NK : 1];
     if (FUSED) operands(0, 0);
 #pragma unroll
     for (int k = 0; k < NK; ++k) {
+        if (LNO && KS == 4) vs[k] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
         if (FUSED && k + 1 < NK) operands(k + 1, (k + 1) & 1);
         const int mt = KS == 1 ? k / 4 : k, x = KS == 1 ? k % 4 : wave;
         int64_t off;
@@ -356,7 +368,101 @@ __device__ void body(const GemmArgs &a) {
             st4(o, kx == 0 ? make_float4(v[0], pv[0], v[1], pv[1]) : make_float4(pv[2], v[2], pv[3], v[3]));
             continue;
         }
+        if (LNO && lnw) {
+            if (KS == 1)
+                st4(lt + wave * PER + (mt * 16 + i) * LDT + 16 * x + 4 * g, make_float4(v[0], v[1], v[2], v[3]));
+            else
+                vs[k] = make_float4(v[0], v[1], v[2], v[3]);
+            if (!a.lo.keep) continue;
+        }
         st4(Y + placed(off), make_float4(v[0], v[1], v[2], v[3]));
+    }
+    if constexpr (LNO) {
+        // Per pixel, the LayerNorm's statistics in the LayerNorm kernels'
+        // order (ascending channel, one pass for s1 and s2): the tiles go
+        // through LDS so that one lane reads a pixel's channels in turn; then
+        // every lane normalises the values it holds with the LayerNorm's
+        // expression. The LayerNorm's G * TW channels are the tiles of G
+        // consecutive waves of one block (G = lo.group; G = 1 with KS = 4).
+        // With G = 1 the exchange stays within the wave (its own LDS rows)
+        // and needs no block barrier; with G > 1 every wave of a block that
+        // holds a group takes both barriers (block-uniform, and the host
+        // launches whole blocks of tiles, so no wave has left early).
+        const int G = KS == 1 ? a.lo.group : 1;
+        bool any = lnw;
+        if (KS == 1 && G > 1) {
+            any = false;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int bw = ((unit * 4 + j) % nib) * TW;
+                any = any || (bw >= a.lo.row0 && bw < a.lo.row0 + G * TW);
+            }
+        }
+        if (any) {
+            float *t;
+            if constexpr (KS == 1) {
+                t = lt + wave * PER;
+            } else {
+                static_assert(4 * PER <= 4 * NACC * 64, "the reduction buffer holds the exchange");
+                __syncthreads();  // every wave has read its sums out of red
+                t = red + wave * PER;
+#pragma unroll
+                for (int k = 0; k < NK; ++k) st4(t + (k * 16 + i) * LDT + 4 * g, vs[k]);
+            }
+            auto sync = [&]() {
+                if (G > 1) {
+                    __syncthreads();
+                } else {
+                    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+                    __builtin_amdgcn_wave_barrier();
+                    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+                }
+            };
+            const int lq = lnw ? (w0 - a.lo.row0) / TW : 0;  // place in the group
+            sync();
+            if (lnw && lq == 0 && lane < PC) {
+                float s1 = 0.0f, s2 = 0.0f;
+                for (int q = 0; q < G; ++q) {
+#pragma unroll 8
+                    for (int c = 0; c < TW; ++c) {
+                        const float v = t[q * PER + c * LDT + lane];
+                        s1 += v;
+                        s2 += v * v;
+                    }
+                }
+                const float nf = (float)(G * TW);
+                const float m = s1 / nf;
+                const float var = s2 / nf - m * m;
+                t[TW * LDT + lane] = m;
+                t[TW * LDT + PC + lane] = 1.0f / sqrtf(fmaxf(var, 0.0f) + a.lo.eps);
+            }
+            sync();
+            if (lnw) {
+                const float *ts = t - lq * PER + TW * LDT;  // the group's statistics
+                float lw[TMW], lb[TMW];
+#pragma unroll
+                for (int mt = 0; mt < TMW; ++mt) {
+                    lw[mt] = a.lo.scale[lq * TW + mt * 16 + i];
+                    lb[mt] = a.lo.bias[lq * TW + mt * 16 + i];
+                }
+                float *ly = a.lo.y - (int64_t)a.lo.row0 * N;  // indexed like Y (one batch)
+#pragma unroll
+                for (int k = 0; k < NK; ++k) {
+                    const int mt = KS == 1 ? k / 4 : k, x = KS == 1 ? k % 4 : 0;
+                    int64_t off;
+                    if (!where(k, off)) continue;
+                    const float4 m4 = ld4(ts + 16 * x + 4 * g);
+                    const float4 r4 = ld4(ts + PC + 16 * x + 4 * g);
+                    const float w = lw[mt], c = lb[mt];
+                    float4 y = ld4(t + (mt * 16 + i) * LDT + 16 * x + 4 * g);
+                    y.x = (y.x - m4.x) * r4.x * w + c;
+                    y.y = (y.y - m4.y) * r4.y * w + c;
+                    y.z = (y.z - m4.z) * r4.z * w + c;
+                    y.w = (y.w - m4.w) * r4.w * w + c;
+                    st4(ly + off, y);
+                }
+            }
+        }
     }
 }
 
@@ -385,6 +491,12 @@ __device__ void body(const GemmArgs &a) {
     extern "C" __global__ __launch_bounds__(256) void mx_pw_ch##TMW##SUF##_t(GemmArgs a) {          \
         pw::body<pw::CH, TMW, KS, false, false, false, false, true>(a);                             \
     }
+// mx_pw_ch<TMW>[_k4][_ln]_f_lo: with a LayerNorm of one wave-wide band of
+// the output rows (GemmArgs lo).
+#define MXK_PW_LO(TMW, KS, LN, SUF)                                                               \
+    extern "C" __global__ __launch_bounds__(256) void mx_pw_ch##TMW##SUF##_f_lo(GemmArgs a) {      \
+        pw::body<pw::CH, TMW, KS, true, LN, false, false, false, true>(a);                          \
+    }
 #define MXK_PW_MUL(TMW) \
     MXK_PW2(ch, CH, TMW, 1, false, false, true, _mul) MXK_PW2(ch, CH, TMW, 4, false, false, true, _k4_mul)
 MXK_PW(ch, CH, 1)
@@ -405,3 +517,11 @@ MXK_PW_CT(2, 1, )
 MXK_PW_CT(2, 4, _k4)
 MXK_PW_CT(4, 1, )
 MXK_PW_CT(4, 4, _k4)
+MXK_PW_LO(2, 1, false, )
+MXK_PW_LO(2, 4, false, _k4)
+MXK_PW_LO(2, 1, true, _ln)
+MXK_PW_LO(2, 4, true, _k4_ln)
+MXK_PW_LO(4, 1, false, )
+MXK_PW_LO(4, 4, false, _k4)
+MXK_PW_LO(4, 1, true, _ln)
+MXK_PW_LO(4, 4, true, _k4_ln)

@@ -329,12 +329,21 @@ class CustomPlan:
 
     This is what any host that owns its own plan does at the boundary: fill an
     mx_plan_desc from its own arrays. Used for the isolated-op configurations.
+    `views` = {buffer: (parent, delta)} makes a buffer a view of an earlier
+    one (at `delta` elements into it) and hands the executor the view table,
+    so it lays out its own device arena as it does for a built plan.
     """
 
-    def __init__(self, bufs, ops, weights, input=0, output=None, align=64):
+    def __init__(self, bufs, ops, weights, input=0, output=None, align=64, views=None):
         self.bufs = [tuple(int(v) for v in b) for b in bufs]
+        views = views or {}
         offs, off = [], 0
-        for c, h, w in self.bufs:
+        for i, (c, h, w) in enumerate(self.bufs):
+            if i in views:
+                par, delta = views[i]
+                assert par < i and delta + c * h * w <= self.buf_len_of(par), "a view inside an earlier buffer"
+                offs.append(offs[par] + delta)
+                continue
             offs.append(off)
             off += c * h * w
             off = (off + align - 1) // align * align
@@ -355,8 +364,17 @@ class CustomPlan:
         d.n_bufs, d.bufs, d.offs = len(bufs), self._bufs, self._offs
         d.n_weights, d.weights, d.weight_lens = len(self._weights), self._wptr, self._wlen
         d.arena_len, d.input, d.output = self.arena_len, self.input, self.output
+        if views:
+            nb = len(self.bufs)
+            self._apar = (C.c_int64 * nb)(*[views[i][0] if i in views else -1 for i in range(nb)])
+            self._adel = (C.c_uint64 * nb)(*[views[i][1] if i in views else 0 for i in range(nb)])
+            d.alias_parent, d.alias_delta = self._apar, self._adel
         self.desc = d
         self.shape = self.bufs[self.input]
+
+    def buf_len_of(self, i):
+        c, h, w = self.bufs[i]
+        return c * h * w
 
     def buf_len(self, i):
         c, h, w = self.bufs[i]

@@ -377,3 +377,111 @@ def test_transposed_conv_edges(gpu_ok, ci, co, h, w):
     streaming = w % 4 == 0 and ci % 16 == 0
     assert steps[0][2].startswith("mx_pw_ch" if streaming else "mx_gemm_") and steps[0][2].endswith("_t"), steps
     check(got, O.convt2x2(x, wt, b), "convt %d->%d @%dx%d" % (ci, co, h, w))
+
+
+@pytest.mark.parametrize("c,h,w,ln_in", [
+    (32, 16, 40, False),   # level-0 gate: c -> 2c + GELU, LayerNorm of the v half
+    (32, 12, 52, True),    # with the input LayerNorm folded too (the real level-0 step)
+    (64, 8, 36, True),     # 64 channels, few tiles (split reduction): one 64-wide wave
+    (64, 128, 256, True),  # 64 channels, 2048 tiles: two 32-wide waves of a block per pixel tile
+    (128, 32, 64, False),  # 128 channels, K 128 (split reduction): the LayerNorm on its own
+    (64, 130, 260, False),  # 33800 pixels: a partial last tile for a two-wave group
+    (32, 5, 28, False),    # 140 pixels: the last 64-pixel tile partial
+])
+def test_layernorm_of_the_gate_half_in_the_epilogue(gpu_ok, c, h, w, ln_in):
+    """[ChanLn ->] Conv1x1 c->2c -> Gelu -> ChanLn of channels c..2c (a view):
+    one streaming launch whose v-half waves normalise their tile and store only
+    the LayerNorm (nothing else reads the raw half). Bitwise the unfused pass
+    (the LayerNorm's own order and expression), the CPU path to the GEMM bar."""
+    from maxim_amd import plan as P
+    from maxim_amd import hip as H
+    rng = np.random.default_rng(c * 100 + h + w)
+    hw = h * w
+    X, XN, T, G, V, LN = range(6)
+    bufs = [(c, h, w), (c, h, w), (2 * c, h, w), (2 * c, h, w), (c, h, w), (c, h, w)]
+    views = {V: (G, c * hw)}
+    wt = he(rng, (2 * c, c), c)
+    b = (rng.standard_normal(2 * c) * 0.1).astype(np.float32)
+    g1 = (1 + 0.1 * rng.standard_normal(c)).astype(np.float32)
+    b1 = (0.1 * rng.standard_normal(c)).astype(np.float32)
+    g2 = (1 + 0.1 * rng.standard_normal(c)).astype(np.float32)
+    b2 = (0.1 * rng.standard_normal(c)).astype(np.float32)
+    ops = []
+    if ln_in:
+        ops.append(P.make_op(P.CHAN_LN, dst=XN, src=X, scale=3, bias=4, c=c, hw=hw))
+    ops += [P.make_op(P.CONV1X1, dst=T, src=XN if ln_in else X, w=0, bias=1, c_in=c, c_out=2 * c, h=h, wd=w),
+            P.make_op(P.GELU, dst=G, src=T, n=2 * c * hw),
+            P.make_op(P.CHAN_LN, dst=LN, src=V, scale=5, bias=6, c=c, hw=hw)]
+    cp = P.CustomPlan(bufs, ops, [wt, b, np.zeros(1, np.float32), g1, b1, g2, b2], input=X, output=LN, views=views)
+    x = rng.standard_normal(bufs[X]).astype(np.float32)
+    gpu = H.Gpu(cp)
+    gpu.write_buf(X, x)
+    gpu.run_ops(0, len(ops))
+    steps = gpu.steps()
+    got_ln = gpu.read_buf(LN).reshape(bufs[LN])
+    got_u = gpu.read_buf(G).reshape(bufs[G])[:c]
+    gpu.set_fusion(False)
+    gpu.run_ops(0, len(ops))
+    plain_ln = gpu.read_buf(LN).reshape(bufs[LN])
+    plain_u = gpu.read_buf(G).reshape(bufs[G])[:c]
+    gpu.close()
+    print("steps", steps)
+    if c == 128:
+        kernels = [k for _, k in H.Gpu(cp).launches()]
+        assert len(steps) == 1 and kernels[-1].startswith("mx_chan_ln"), kernels
+    else:
+        assert len(steps) == 1 and steps[0][2].endswith("_f_lo"), steps
+    assert np.array_equal(got_ln.view(np.uint32), plain_ln.view(np.uint32)), "fused and unfused LayerNorm differ"
+    assert np.array_equal(got_u.view(np.uint32), plain_u.view(np.uint32)), "fused and unfused u half differ"
+    want_ln = oracle_plan(cp, {X: x}, LN)
+    want_g = oracle_plan(cp, {X: x}, G)
+    check(got_u, want_g[:c], "u half c=%d @%dx%d" % (c, h, w))
+    # the LayerNorm scales the GEMM's rounding by 1/std of each pixel: an
+    # absolute bar on its unit-variance output
+    err = float(np.abs(got_ln.astype(np.float64) - want_ln).max())
+    print("LayerNorm max-abs vs CPU %.3g" % err)
+    assert err <= 1e-3, err
+
+
+@pytest.mark.parametrize("c,k,h,w", [
+    (32, 64, 16, 40),    # level-0 out-projection + residual, then the RCAB LayerNorm
+    (64, 128, 16, 40),   # K 128 (split reduction): one 64-wide wave
+    (64, 64, 256, 256),  # K 64, 1024 pixel tiles: two 32-wide waves per pixel tile
+    (32, 64, 3, 44),     # 132 pixels: a partial tile
+])
+def test_layernorm_of_the_residual_sum_in_the_epilogue(gpu_ok, c, k, h, w):
+    """Conv1x1 k->c -> Add -> ChanLn, the raw sum also read later (kept): the
+    streaming launch stores the sum and its LayerNorm. Bitwise the unfused
+    pass, the CPU path to the GEMM bar."""
+    from maxim_amd import plan as P
+    from maxim_amd import hip as H
+    rng = np.random.default_rng(c + k + h * w)
+    hw = h * w
+    X, R, T, Y, LN, Z = range(6)
+    bufs = [(k, h, w), (c, h, w), (c, h, w), (c, h, w), (c, h, w), (c, h, w)]
+    wt = he(rng, (c, k), k)
+    b = (rng.standard_normal(c) * 0.1).astype(np.float32)
+    g2 = (1 + 0.1 * rng.standard_normal(c)).astype(np.float32)
+    b2 = (0.1 * rng.standard_normal(c)).astype(np.float32)
+    n = c * hw
+    ops = [P.make_op(P.CONV1X1, dst=T, src=X, w=0, bias=1, c_in=k, c_out=c, h=h, wd=w),
+           P.make_op(P.ADD, dst=Y, src=T, src2=R, n=n),
+           P.make_op(P.CHAN_LN, dst=LN, src=Y, scale=2, bias=3, c=c, hw=hw),
+           P.make_op(P.ADD, dst=Z, src=LN, src2=Y, n=n)]
+    cp = P.CustomPlan(bufs, ops, [wt, b, g2, b2], input=X, output=Z)
+    inputs = {X: rng.standard_normal(bufs[X]).astype(np.float32), R: rng.standard_normal(bufs[R]).astype(np.float32)}
+    got, steps = run_plan(cp, inputs, Z)
+    print("steps", steps)
+    assert any(s[2].endswith("_f_lo") for s in steps), steps
+    gpu = H.Gpu(cp)
+    for bb, v in inputs.items():
+        gpu.write_buf(bb, v)
+    gpu.set_fusion(False)
+    gpu.run_ops(0, len(ops))
+    plain = gpu.read_buf(Z).reshape(bufs[Z])
+    gpu.close()
+    assert np.array_equal(got.view(np.uint32), plain.view(np.uint32)), "fused and unfused passes differ"
+    want = oracle_plan(cp, inputs, Z)
+    err = float(np.abs(got.astype(np.float64) - want).max())
+    print("max-abs vs CPU %.3g" % err)
+    assert err <= 1e-3, err
