@@ -92,7 +92,8 @@ int mxh_read_into(mxh_gpu *g, uint64_t off, float *out, uint64_t n);
 int mxh_read_arena(mxh_gpu *g, float *out, uint64_t n);
 /* `n` floats to device-arena element `off`. */
 int mxh_write_into(mxh_gpu *g, uint64_t off, const float *in, uint64_t n);
-/* MAXIM_POISON (src/exec_gpu.rs:320-340): fill the whole arena with 0xCD bytes. */
+/* MAXIM_POISON (src/exec_gpu.rs:320-340): fill the whole arena, and the
+ * executor's scratch (partial sums, LayerNorm statistics), with 0xCD bytes. */
 int mxh_poison(mxh_gpu *g);
 /* Wait for all queued work. */
 int mxh_sync(mxh_gpu *g);

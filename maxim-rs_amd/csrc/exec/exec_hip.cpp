@@ -52,6 +52,11 @@ struct Step {
     uint64_t first, last;
     std::vector<Launch> launches;
     size_t main = 0;  // the launch that names the step in reports
+    // A folded LayerNorm whose statistics step so_from's epilogue writes:
+    // when a run of ops starts after that step, `pre` (the statistics pass)
+    // runs first.
+    int64_t so_from = -1;
+    std::vector<Launch> pre;
 };
 
 template <typename T>
@@ -281,6 +286,14 @@ struct StepSpec {
     // band is read elsewhere too, so it is still stored.
     int64_t lno = -1;
     bool lno_keep = true;
+    // LayerNorm statistics from the epilogue (_lo, mode 1). Producer:
+    // so_nband bands of so_c channels from output row so_row0, written at
+    // so_out of the statistics region as [band][2][so_hw]. Consumer (a step
+    // with a folded LayerNorm): its statistics at so_in, from step so_from,
+    // when that step's kernel took them.
+    int64_t so_row0 = -1, so_c = 0, so_from = -1;
+    int so_nband = 0;
+    uint64_t so_hw = 0, so_out = 0, so_in = 0;
 };
 
 struct Program {
@@ -290,6 +303,7 @@ struct Program {
     std::vector<uint64_t> doff;     // device element offset of every buffer
     uint64_t arena_len = 0;
     uint64_t fused_ops = 0;
+    uint64_t so_len = 0;  // floats of the LayerNorm statistics region
     bool repacked = false;
     void plan_fusion(const mx_plan_desc *p, bool require_clear);
     void layout(const mx_plan_desc *p, bool repack);
@@ -308,7 +322,7 @@ public:
     unsigned char *wdev = nullptr;
     uint64_t wbytes = 0;
     float *scratch = nullptr;
-    uint64_t scratch_len = 0, ln_off = 0;
+    uint64_t scratch_len = 0, ln_off = 0, so_base = 0;
     uint64_t n_ops = 0, n_bufs = 0;
     std::vector<std::vector<Launch>> ops;
     uint64_t launched = 0, kernels = 0;
@@ -370,6 +384,8 @@ public:
         for (const Step &st : prog) {
             if (st.last <= first || st.first >= last) continue;
             if (st.first >= first && st.last <= last) {
+                if (st.so_from >= 0 && prog[st.so_from].first < first)
+                    for (auto &l : st.pre) launch(const_cast<Launch &>(l));
                 for (auto &l : st.launches) launch(const_cast<Launch &>(l));
                 launched += st.last - st.first;
             } else {
@@ -758,7 +774,9 @@ Gpu::Gpu(const mx_plan_desc *p) : H(hip()), doff(pg.doff) {
     uint64_t ln_need = 0;
     for (const StepSpec &sp : pg.specs)
         if (sp.ln >= 0) ln_need = std::max<uint64_t>(ln_need, 2 * (uint64_t)p->ops[sp.ln].hw);
-    scratch_len = std::max<uint64_t>(ln_off + ln_need, 64);
+    // then the statistics that steps' epilogues leave for later steps
+    so_base = (ln_off + ln_need + 63) & ~(uint64_t)63;
+    scratch_len = std::max<uint64_t>(so_base + pg.so_len, 64);
     const uint64_t need = arena_len * 4 + wbytes + scratch_len * 4;
     size_t free_b = 0, total_b = 0;
     if (H.hipMemGetInfo(&free_b, &total_b) == 0 && need > free_b) {
@@ -1597,6 +1615,95 @@ void Program::plan_fusion(const mx_plan_desc *p, bool require_clear) {
         merged.push_back(sp);
     }
     specs.swap(merged);
+
+    // LayerNorm statistics from the producer. A folded LayerNorm's input x
+    // (or, past an elided forward permutation, its source in image order)
+    // is a whole band of output channels of an earlier streaming GEMM step,
+    // and nothing writes it in between: that step's epilogue writes each
+    // pixel's statistics of the band (the statistics pass's values, at the
+    // pixel's image position) and the folded GEMM reads them instead of
+    // running the statistics pass. Each producer's bands share one slot of
+    // the statistics region, live from the producer to its last reader;
+    // slots are packed first-fit over those spans.
+    so_len = 0;
+    if (!std::getenv("MAXIM_NO_LN_EPILOGUE")) {
+        struct Req {
+            uint64_t p = 0, last = 0, hw = 0;
+            int64_t c = 0, lo = -1, hi = -1;
+            std::vector<std::pair<uint64_t, int64_t>> qs;  // (consumer spec, band row)
+        };
+        std::map<uint64_t, Req> reqs;
+        for (uint64_t q = 0; q < specs.size(); ++q) {
+            const StepSpec &Q = specs[q];
+            if (Q.ln < 0) continue;
+            const mx_op &ln = p->ops[Q.ln];
+            if (ln.c != 32 && ln.c != 64 && ln.c != 128) continue;
+            const int64_t X = Q.xperm >= 0 ? Q.xsrc : ln.src;
+            const R xr = range(X);
+            int64_t P = -1;
+            for (int64_t s2 = (int64_t)q - 1; s2 >= 0 && P < 0; --s2)
+                for (uint64_t k = specs[s2].first; k < specs[s2].last && P < 0; ++k)
+                    for (int64_t d : writes_of(p->ops[k]))
+                        if (overlap(range(d), xr)) P = s2;
+            if (P < 0) continue;
+            const StepSpec &S = specs[P];
+            if (S.rule != RULE_NONE || S.lno >= 0 || S.xmul >= 0 || S.xperm >= 0) continue;
+            const uint64_t g = S.ln >= 0 ? S.first + 1 : S.first;
+            const mx_op &c = p->ops[g];
+            if (c.kind != MX_OP_CONV1X1 || c.h * c.wd <= 1) continue;
+            const int64_t y = S.out >= 0 ? S.out : c.dst;
+            const uint64_t hw = (uint64_t)(c.h * c.wd);
+            const R yr = range(y);
+            if (ln.hw != (int64_t)hw || xr.a < yr.a || xr.b > yr.b || (xr.a - yr.a) % hw ||
+                xr.b - xr.a != (uint64_t)ln.c * hw)
+                continue;
+            const int64_t row = (int64_t)((xr.a - yr.a) / hw);
+            if (row % ln.c) continue;
+            Req &r = reqs[(uint64_t)P];
+            if (r.c && r.c != ln.c) continue;
+            r.p = (uint64_t)P;
+            r.c = ln.c;
+            r.hw = hw;
+            r.lo = r.lo < 0 ? row : std::min(r.lo, row);
+            r.hi = std::max(r.hi, row + ln.c);
+            r.last = std::max<uint64_t>(r.last, q);
+            r.qs.push_back({q, row});
+        }
+        struct Slot {
+            uint64_t a, b, off, len;
+        };
+        std::vector<Slot> slots;
+        for (auto &kv : reqs) {
+            Req &r = kv.second;
+            const int nband = (int)((r.hi - r.lo) / r.c);
+            const uint64_t len = ((uint64_t)nband * 2 * r.hw + 63) & ~(uint64_t)63;
+            std::vector<uint64_t> cands{0};
+            for (const Slot &t : slots) cands.push_back(t.off + t.len);
+            std::sort(cands.begin(), cands.end());
+            uint64_t off = 0;
+            for (uint64_t cand : cands) {
+                bool clash = false;
+                for (const Slot &t : slots)
+                    if (t.a <= r.last && r.p <= t.b && cand < t.off + t.len && t.off < cand + len) clash = true;
+                if (!clash) {
+                    off = cand;
+                    break;
+                }
+            }
+            slots.push_back({r.p, r.last, off, len});
+            so_len = std::max(so_len, off + len);
+            StepSpec &S = specs[r.p];
+            S.so_row0 = r.lo;
+            S.so_c = r.c;
+            S.so_nband = nband;
+            S.so_hw = r.hw;
+            S.so_out = off;
+            for (const auto &qr : r.qs) {
+                specs[qr.first].so_from = (int64_t)r.p;
+                specs[qr.first].so_in = off + (uint64_t)((qr.second - r.lo) / r.c) * 2 * r.hw;
+            }
+        }
+    }
 }
 
 // The device arena: the plan's own packing rule (largest first, first use as
@@ -1811,76 +1918,91 @@ void Gpu::build_program(const mx_plan_desc *p) {
     // step's kernel cannot take it (not streaming, another operand form, a
     // misaligned or overlapping LayerNorm output), the LayerNorm's own
     // launch after the step's.
-    auto lno_apply = [&](const StepSpec &sp, Step &st) {
-        if (sp.lno < 0) return;
-        const mx_op &ln = p->ops[sp.lno];
+    // The streaming kernel's _lo form on a step's main launch: LayerNorm
+    // bands of c channels from output row r0 (mode 0: one band, normalised
+    // into y; mode 1: nband bands' statistics into y). False where the launch
+    // cannot take it (not streaming, another operand form, a misaligned or
+    // overlapping y, a tile that cannot hold the band).
+    auto lo_apply = [&](Step &st, int mode, int64_t r0, int64_t c, int nband, int keep, float *y, int64_t ylen,
+                        const float *scale, const float *bias, float eps, bool need_ymap) -> bool {
         Launch &l = st.launches[st.main];
-        std::string nm = l.name;
+        if (strncmp(l.name, "mx_pw_ch", 8) || l.kind != 1 || !aligned(y, 16)) return false;
+        const std::string nm = l.name;
         GemmArgs a;
         memcpy(&a, l.a0, sizeof a);
-        ChanLnArgs la;
-        memcpy(&la, ops[sp.lno][0].a0, sizeof la);
-        bool ok = !strncmp(l.name, "mx_pw_ch", 8) && l.kind == 1 && a.batch == 1 && !a.ymap.on && a.N == ln.hw &&
-                  aligned(la.y, 16);
-        const bool lnn = nm.find("_ln") != std::string::npos;
-        if (ok) {
-            // the name is mx_pw_ch<T>[_k4][_ln][_f]: nothing else may be folded in
-            std::string rest = nm.substr(9);
-            for (const char *t : {"_k4", "_ln", "_f"})
-                if (!rest.compare(0, strlen(t), t)) rest = rest.substr(strlen(t));
-            ok = rest.empty();
-        }
-        const int64_t row0 = ok ? (la.x - a.C) : -1;
-        ok = ok && row0 >= 0 && row0 % a.N == 0 && (row0 / a.N) % ln.c == 0 && row0 / a.N + ln.c <= a.M;
-        if (ok) {
-            // the LayerNorm's output may overlap nothing the kernel reads or writes
-            const float *lo = la.y, *hi = la.y + ln.c * ln.hw;
-            auto clash = [&](const float *b, int64_t n) { return b && b < hi && lo < b + n; };
-            const int64_t xn = (int64_t)a.K * a.N;
-            ok = !clash(a.C, (int64_t)a.M * a.N) && !clash(a.B, xn) && !clash(a.B2, xn) &&
-                 !clash(a.e.u, (int64_t)a.M * a.N) && !clash(a.e.r1, (int64_t)a.M * a.N) &&
-                 !clash(a.e.r2, (int64_t)a.M * a.N) && !clash(a.A, (int64_t)a.M * a.K);
-            if (ok && a.xmap.on) ok = !clash(a.B, a.xmap.plane * a.K);
-            if (ok && a.ln.mean) ok = !clash(a.ln.mean, 2 * (int64_t)a.N);
-        }
-        if (!ok) {
-            for (const Launch &x : ops[sp.lno]) st.launches.push_back(x);
-            return;
-        }
-        // The tile: the step's own width when G = C / width consecutive
-        // waves of a block hold the band (G = 1 also with the split
-        // reduction; G > 1 needs whole blocks of tiles, groups aligned to
-        // the block), else a width of C itself. The reduction split stays
-        // as the step has it: the tile width does not change any output's
-        // order of accumulation, the split does, and the fused pass stays
-        // the unfused one to the bit.
-        const int r0 = (int)(row0 / a.N);
+        if (a.batch != 1 || (mode == 0 && a.ymap.on) || (need_ymap && !a.ymap.on)) return false;
+        // the name is mx_pw_ch<T>[_k4][_ln][_f]: nothing else may be folded in
+        std::string rest = nm.substr(9);
+        for (const char *t : {"_k4", "_ln", "_f"})
+            if (!rest.compare(0, strlen(t), t)) rest = rest.substr(strlen(t));
+        if (!rest.empty() || r0 < 0 || r0 % c || r0 + nband * c > a.M) return false;
+        // y may overlap nothing the kernel reads or writes
+        const float *lo = y, *hi = y + ylen;
+        auto clash = [&](const float *b, int64_t n) { return b && b < hi && lo < b + n; };
+        const int64_t xn = (int64_t)a.K * a.N, yn = (int64_t)a.M * a.N;
+        if (clash(a.C, a.ymap.on ? std::max<int64_t>(yn, a.ymap.plane * a.M) : yn) || clash(a.B, xn) ||
+            clash(a.B2, xn) || clash(a.e.u, yn) || clash(a.e.r1, yn) || clash(a.e.r2, yn) ||
+            clash(a.A, (int64_t)a.M * a.K) || (a.xmap.on && clash(a.B, a.xmap.plane * a.K)) ||
+            (a.ln.mean && clash(a.ln.mean, 2 * (int64_t)a.N)))
+            return false;
+        // The tile: the step's own width when G = c / width consecutive
+        // waves of a block hold a band (G = 1 also with the split reduction;
+        // G > 1 needs whole blocks of tiles, groups aligned to the block),
+        // else a width of c itself. The reduction split stays as the step
+        // has it: the tile width does not change any output's order of
+        // accumulation, the split does, and the fused pass stays the unfused
+        // one to the bit.
         auto fits = [&](int tmw, bool k4) {
-            const int tw = 16 * tmw, G = (int)(ln.c / tw);
-            if (ln.c % tw || (G != 1 && G != 2 && G != 4) || (k4 && G != 1)) return 0;
+            const int tw = 16 * tmw, G = (int)(c / tw);
+            if (c % tw || (G != 1 && G != 2 && G != 4) || (k4 && G != 1)) return 0;
             const int64_t nib = (a.M + tw - 1) / tw, tiles = nib * ((a.N + 63) / 64);
             if (G > 1 && (nib % G || (r0 / tw) % G || tiles % 4)) return 0;
             return G;
         };
-        const int tmw0 = nm[8] - '0';
-        const bool k40 = nm.find("_k4") != std::string::npos;
-        const bool k4 = k40;
-        int tmw = tmw0, G = fits(tmw0, k4);
-        if (!G && (ln.c == 32 || ln.c == 64)) {
-            tmw = (int)(ln.c / 16);
+        const bool k4 = nm.find("_k4") != std::string::npos, lnn = nm.find("_ln") != std::string::npos;
+        int tmw = nm[8] - '0', G = fits(tmw, k4);
+        if (!G && (c == 32 || c == 64)) {
+            tmw = (int)(c / 16);
             G = 1;
         }
-        if (!G) {
-            for (const Launch &x : ops[sp.lno]) st.launches.push_back(x);
-            return;
-        }
+        if (!G) return false;
         const int64_t tiles = ((a.M + 16 * tmw - 1) / (16 * tmw)) * ((a.N + 63) / 64);
         l.name = intern("mx_pw_ch" + std::to_string(tmw) + (k4 ? "_k4" : "") + (lnn ? "_ln" : "") + "_f_lo");
         l.f = fn(l.name);
         l.g[0] = (unsigned)(k4 ? tiles : (tiles + 3) / 4);
         l.g[1] = 1;
-        a.lo = LnOut{la.scale, la.bias, la.y, la.eps, r0, sp.lno_keep ? 1 : 0, G};
+        a.lo = LnOut{scale, bias, y, eps, (int32_t)r0, keep, G, mode, nband, 0};
         set_args(l, a);
+        return true;
+    };
+    // A GEMM step that also computes the LayerNorm of an output band (lno),
+    // or, where its kernel cannot, the LayerNorm's own launch after it.
+    auto lno_apply = [&](const StepSpec &sp, Step &st) {
+        if (sp.lno < 0) return;
+        const mx_op &ln = p->ops[sp.lno];
+        ChanLnArgs la;
+        memcpy(&la, ops[sp.lno][0].a0, sizeof la);
+        const Launch &l = st.launches[st.main];
+        GemmArgs a;
+        memcpy(&a, l.a0, sizeof a);
+        const int64_t d = l.kind == 1 ? la.x - a.C : -1;
+        const int64_t r0 = d >= 0 && d % ln.hw == 0 && a.N == ln.hw ? d / ln.hw : -1;
+        if (!lo_apply(st, 0, r0, ln.c, 1, sp.lno_keep ? 1 : 0, la.y, ln.c * ln.hw, la.scale, la.bias, la.eps, false))
+            for (const Launch &x : ops[sp.lno]) st.launches.push_back(x);
+    };
+    // A GEMM step whose output bands later LayerNorms fold (so_*): their
+    // statistics from its epilogue, into the statistics region.
+    std::vector<char> so_ok(pg.specs.size(), 0);
+    auto so_apply = [&](const StepSpec &sp, Step &st) {
+        if (sp.so_nband <= 0) return;
+        const int64_t hw = (int64_t)sp.so_hw;
+        const Launch &l = st.launches[st.main];
+        GemmArgs a;
+        memcpy(&a, l.a0, sizeof a);
+        if (l.kind != 1 || a.N != hw) return;
+        so_ok[&sp - pg.specs.data()] =
+            lo_apply(st, 1, sp.so_row0, sp.so_c, sp.so_nband, 1, scratch + so_base + sp.so_out,
+                     2 * hw * sp.so_nband, nullptr, nullptr, mx::kEps, sp.perm >= 0);
     };
     prog.clear();
     for (const StepSpec &sp : pg.specs) {
@@ -1960,6 +2082,7 @@ void Gpu::build_program(const mx_plan_desc *p) {
             if (sp.xperm >= 0) token_map(sp, v[0]);
             Step st{sp.first, sp.last, v};
             lno_apply(sp, st);
+            so_apply(sp, st);
             prog.push_back(st);
             continue;
         }
@@ -1985,9 +2108,14 @@ void Gpu::build_program(const mx_plan_desc *p) {
             st.main = st.launches.size();
             for (const Launch &x : gp) st.launches.push_back(x);
             lno_apply(sp, st);
+            so_apply(sp, st);
             prog.push_back(st);
             continue;
         }
+        // statistics from the step that produced x (its _lo epilogue), or
+        // a statistics pass here
+        const bool so = sp.so_from >= 0 && so_ok[sp.so_from];
+        if (so) stats = scratch + so_base + sp.so_in;
         ChanLnArgs sa = la;
         sa.y = stats;
         Launch sl;
@@ -2015,10 +2143,17 @@ void Gpu::build_program(const mx_plan_desc *p) {
             a.xmap = BlockMap{q.h * q.wd, 1, (int32_t)q.p[2], (int32_t)q.p[3], (int32_t)q.p[1], (int32_t)q.wd, 0};
         }
         set_args(gl, a);
-        Step st{sp.first, sp.last, {sl}};
+        Step st{sp.first, sp.last, {}};
+        if (so) {
+            st.so_from = sp.so_from;
+            st.pre.push_back(sl);
+        } else {
+            st.launches.push_back(sl);
+        }
+        st.main = st.launches.size();
         for (const Launch &x : gp) st.launches.push_back(x);
-        st.main = 1;
         lno_apply(sp, st);
+        so_apply(sp, st);
         prog.push_back(st);
     }
 }
@@ -2251,6 +2386,7 @@ int mxh_write_into(mxh_gpu *g, uint64_t off, const float *in, uint64_t n) {
 int mxh_poison(mxh_gpu *g) {
     return guard([&] {
         mxh::check(G(g)->H.hipMemsetD8Async(G(g)->arena, 0xCD, G(g)->arena_len * 4, G(g)->stream), "poison");
+        mxh::check(G(g)->H.hipMemsetD8Async(G(g)->scratch, 0xCD, G(g)->scratch_len * 4, G(g)->stream), "poison");
         G(g)->sync();
     });
 }

@@ -156,16 +156,20 @@ struct BlockMap {
 };
 
 // A channel LayerNorm of a channel-major GEMM's output (the streaming
-// kernels' _lo form, one batch): output rows row0 .. row0 + C - 1, C being
-// the tile width of `group` consecutive waves of a block, are normalised per
-// pixel with the LayerNorm kernels' order and expression and written to y as
-// [C][N]; keep = 0 leaves those rows' raw values unstored (nothing else
-// reads them).
+// kernels' _lo form, one batch): bands of C output rows from row0 on, C
+// being the tile width of `group` consecutive waves of a block.
+//   mode 0: one band, normalised per pixel with the LayerNorm kernels' order
+//       and expression and written to y as [C][N]; keep = 0 leaves the
+//       band's raw values unstored (nothing else reads them).
+//   mode 1: `nband` bands, each pixel's statistics only (mean, then 1/std,
+//       the LayerNorm statistics kernels' values) written to y as
+//       [nband][2][N] at the pixel's image position (through ymap), for the
+//       GEMMs that fold those LayerNorms later; the output is stored as usual.
 struct LnOut {
     const float *scale, *bias;
     float *y;
     float eps;
-    int32_t row0, keep, group;
+    int32_t row0, keep, group, mode, nband, pad;
 };
 
 struct GemmArgs {

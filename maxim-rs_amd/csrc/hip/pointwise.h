@@ -285,7 +285,8 @@ __device__ void body(const GemmArgs &a) {
     constexpr int LDT = PC + 4;            // padded LDS row
     constexpr int PER = TW * LDT + 2 * PC;  // LDS floats per wave
     __shared__ float lt[LNO && KS == 1 ? 4 * PER : 1];
-    const bool lnw = LNO && w0 >= a.lo.row0 && w0 < a.lo.row0 + (KS == 1 ? a.lo.group : 1) * TW;
+    const int lnspan = (KS == 1 ? a.lo.group : 1) * TW * a.lo.nband;  // rows with a LayerNorm
+    const bool lnw = LNO && w0 >= a.lo.row0 && w0 < a.lo.row0 + lnspan;
     float4 vs[LNO && KS == 4 ? NK : 1];
     if (FUSED) operands(0, 0);
 #pragma unroll
@@ -382,8 +383,9 @@ __device__ void body(const GemmArgs &a) {
         // order (ascending channel, one pass for s1 and s2): the tiles go
         // through LDS so that one lane reads a pixel's channels in turn; then
         // every lane normalises the values it holds with the LayerNorm's
-        // expression. The LayerNorm's G * TW channels are the tiles of G
-        // consecutive waves of one block (G = lo.group; G = 1 with KS = 4).
+        // expression (mode 0), or writes the statistics (mode 1). A band's
+        // G * TW channels are the tiles of G consecutive waves of one block
+        // (G = lo.group; G = 1 with KS = 4).
         // With G = 1 the exchange stays within the wave (its own LDS rows)
         // and needs no block barrier; with G > 1 every wave of a block that
         // holds a group takes both barriers (block-uniform, and the host
@@ -395,7 +397,7 @@ __device__ void body(const GemmArgs &a) {
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
                 const int bw = ((unit * 4 + j) % nib) * TW;
-                any = any || (bw >= a.lo.row0 && bw < a.lo.row0 + G * TW);
+                any = any || (bw >= a.lo.row0 && bw < a.lo.row0 + lnspan);
             }
         }
         if (any) {
@@ -418,7 +420,8 @@ __device__ void body(const GemmArgs &a) {
                     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
                 }
             };
-            const int lq = lnw ? (w0 - a.lo.row0) / TW : 0;  // place in the group
+            const int band = lnw ? (w0 - a.lo.row0) / (G * TW) : 0;
+            const int lq = lnw ? (w0 - a.lo.row0) / TW - band * G : 0;  // place in the group
             sync();
             if (lnw && lq == 0 && lane < PC) {
                 float s1 = 0.0f, s2 = 0.0f;
@@ -433,11 +436,22 @@ __device__ void body(const GemmArgs &a) {
                 const float nf = (float)(G * TW);
                 const float m = s1 / nf;
                 const float var = s2 / nf - m * m;
-                t[TW * LDT + lane] = m;
-                t[TW * LDT + PC + lane] = 1.0f / sqrtf(fmaxf(var, 0.0f) + a.lo.eps);
+                const float r = 1.0f / sqrtf(fmaxf(var, 0.0f) + a.lo.eps);
+                if (a.lo.mode) {  // the statistics only, at the pixel's image position
+                    const int n = s0 + (KS == 1 ? lane : 16 * wave + lane);
+                    if (n < N) {
+                        float *sy = a.lo.y + (int64_t)band * 2 * N;
+                        const int64_t at = placed(n);
+                        sy[at] = m;
+                        sy[N + at] = r;
+                    }
+                } else {
+                    t[TW * LDT + lane] = m;
+                    t[TW * LDT + PC + lane] = r;
+                }
             }
-            sync();
-            if (lnw) {
+            if (!a.lo.mode) sync();
+            if (lnw && !a.lo.mode) {
                 const float *ts = t - lq * PER + TW * LDT;  // the group's statistics
                 float lw[TMW], lb[TMW];
 #pragma unroll

@@ -485,3 +485,65 @@ def test_layernorm_of_the_residual_sum_in_the_epilogue(gpu_ok, c, k, h, w):
     err = float(np.abs(got.astype(np.float64) - want).max())
     print("max-abs vs CPU %.3g" % err)
     assert err <= 1e-3, err
+
+
+@pytest.mark.parametrize("c,k,h,w", [
+    (32, 48, 16, 40),    # one 32-wide wave per band
+    (64, 96, 128, 256),  # two waves of a block per band (2048 pixel tiles)
+    (64, 128, 8, 36),    # split reduction: one 64-wide wave per band
+])
+def test_layernorm_statistics_from_the_producer(gpu_ok, c, k, h, w):
+    """Conv1x1 k->2c, then each half LayerNormed into its own 1x1 conv (the
+    split-head gMLP's two branches) after an unrelated op: the first conv's
+    epilogue writes both halves' statistics and the folded GEMMs read them
+    (no statistics pass). Bitwise the unfused pass; the CPU path to the GEMM
+    bar; a run of ops that starts after the producer runs the statistics pass
+    itself."""
+    from maxim_amd import plan as P
+    from maxim_amd import hip as H
+    rng = np.random.default_rng(c * 7 + k + h * w)
+    hw = h * w
+    X, Y, U, V, UN, VN, A, B, Z1, Z2 = range(10)
+    bufs = [(k, h, w), (2 * c, h, w), (c, h, w), (c, h, w), (c, h, w), (c, h, w),
+            (c, h, w), (c, h, w), (c, h, w), (c, h, w)]
+    views = {U: (Y, 0), V: (Y, c * hw)}
+    wts = [he(rng, (2 * c, k), k), (rng.standard_normal(2 * c) * 0.1).astype(np.float32),
+           he(rng, (c, c), c), (rng.standard_normal(c) * 0.1).astype(np.float32),
+           (1 + 0.1 * rng.standard_normal(c)).astype(np.float32), (0.1 * rng.standard_normal(c)).astype(np.float32),
+           (1 + 0.1 * rng.standard_normal(c)).astype(np.float32), (0.1 * rng.standard_normal(c)).astype(np.float32)]
+    ops = [P.make_op(P.CONV1X1, dst=Y, src=X, w=0, bias=1, c_in=k, c_out=2 * c, h=h, wd=w),
+           P.make_op(P.ADD, dst=A, src=U, src2=V, n=c * hw),          # another reader in between
+           P.make_op(P.CHAN_LN, dst=UN, src=U, scale=4, bias=5, c=c, hw=hw),
+           P.make_op(P.CONV1X1, dst=Z1, src=UN, w=2, bias=3, c_in=c, c_out=c, h=h, wd=w),
+           P.make_op(P.CHAN_LN, dst=VN, src=V, scale=6, bias=7, c=c, hw=hw),
+           P.make_op(P.CONV1X1, dst=Z2, src=VN, w=2, bias=3, c_in=c, c_out=c, h=h, wd=w),
+           P.make_op(P.ADD, dst=B, src=Z1, src2=Z2, n=c * hw)]
+    cp = P.CustomPlan(bufs, ops, wts, input=X, output=B, views=views)
+    x = rng.standard_normal(bufs[X]).astype(np.float32)
+    gpu = H.Gpu(cp)
+    gpu.write_buf(X, x)
+    gpu.run_ops(0, len(ops))
+    steps = gpu.steps()
+    kernels = gpu.launches()
+    got = gpu.read_buf(B).reshape(bufs[B])
+    print("steps", steps)
+    print("launches", kernels)
+    assert steps[0][2].endswith("_f_lo"), steps
+    assert not any(kn.startswith("mx_chan_ln") for _, kn in kernels), kernels
+    # a run starting after the producer: the statistics pass runs itself
+    y_full = gpu.read_buf(Y)
+    gpu.poison()
+    gpu.write_buf(Y, y_full)
+    gpu.run_ops(2, len(ops))
+    part = gpu.read_buf(B).reshape(bufs[B])
+    gpu.set_fusion(False)
+    gpu.write_buf(X, x)
+    gpu.run_ops(0, len(ops))
+    plain = gpu.read_buf(B).reshape(bufs[B])
+    gpu.close()
+    assert np.array_equal(got.view(np.uint32), plain.view(np.uint32)), "fused and unfused passes differ"
+    assert np.array_equal(part.view(np.uint32), plain.view(np.uint32)), "the partial run differs"
+    want = oracle_plan(cp, {X: x}, B)
+    err = float(np.abs(got.astype(np.float64) - want).max())
+    print("max-abs vs CPU %.3g (max|cpu| %.3g)" % (err, float(np.abs(want).max())))
+    assert err <= 1e-3, err
