@@ -220,10 +220,12 @@ struct ConvCfg {
 
 // The mx_c3 tile (c_in % 16 == 0 and >= 128, width % 4 == 0; measured
 // faster than the implicit-GEMM kernel there, slower below): 64 output
-// channels x 4 rows, or 32 x 8 for narrow outputs.
+// channels x 2 rows from 128 output channels on (twice the blocks of 64 x 4
+// at the MAXIM 112x160 shape, 6% faster there), 64 x 4, or 32 x 8 for
+// narrow outputs.
 void pick_c3(ConvCfg &c, int64_t co) {
     c.c3bm = co >= 64 ? 64 : 32;
-    c.c3th = co >= 64 ? 4 : 8;
+    c.c3th = co >= 128 ? 2 : co >= 64 ? 4 : 8;
 }
 
 ConvCfg pick_conv(int64_t co, int64_t ci, int64_t oh, int64_t ow, bool k3, int cus) {

@@ -187,3 +187,4 @@ __device__ void body(const ConvArgs &a) {
     }
 MXK_C3(32, 8, 1, 4)
 MXK_C3(64, 4, 1, 4)
+MXK_C3(64, 2, 2, 2)

@@ -1,6 +1,6 @@
 """Edge shapes of the channel-last 3x3 convolution (mx_c3_*, used from 128
 input channels) against the CPU oracle: image sides that are not a multiple
-of the tile (16 columns, 4 or 8 rows), output-channel counts that leave a
+of the tile (16 columns, 2, 4 or 8 rows), output-channel counts that leave a
 partial block, 128 and 256 input channels, a fused leaky ReLU, and the
 fallbacks to the implicit-GEMM kernel (fewer input channels; a misaligned
 output).
@@ -16,7 +16,8 @@ pytestmark = pytest.mark.gpu
 
 
 @pytest.mark.parametrize("ci,co,h,w", [
-    (128, 128, 20, 28),  # eight chunks, 64-channel blocks, ragged rows and columns
+    (128, 128, 20, 28),  # eight chunks, 64-channel blocks of 2 rows, ragged columns
+    (128, 192, 9, 20),   # three 64-channel blocks of 2 rows, an odd row count
     (128, 40, 9, 20),    # 32-channel blocks of 8 rows, the second block partial
     (256, 64, 7, 12),    # sixteen chunks, a 12-wide image
     (128, 64, 33, 4),    # a 4-wide image
