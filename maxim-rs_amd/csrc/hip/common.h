@@ -33,28 +33,30 @@ __device__ __forceinline__ void xcd_tile(int &tile, int &band) {
 __device__ __forceinline__ float4 ld4(const float *p) { return *reinterpret_cast<const float4 *>(p); }
 __device__ __forceinline__ void st4(float *p, float4 v) { *reinterpret_cast<float4 *>(p) = v; }
 
-// GELU, 0.5 x (1 + erf(x / sqrt 2)), branch-free: erfc(z) for z = |x| / sqrt 2
-// from Abramowitz & Stegun 7.1.28, erfc(z) = (1 + a1 z + ... + a6 z^6)^-16
-// with |error| <= 3e-7, so 1 + erf(x / sqrt 2) is 2 - R for x >= 0 and R for
-// x < 0. Within 2.2e-7 * (1 + |x|) of the exact function, and about a third
-// of the instructions of the device erff (whose two divergent branches both
-// run in a wave of mixed signs). The standalone GELU op and every fused
-// epilogue use this one function, so fusing a GELU changes no bit.
+// GELU, x Phi(x) = 0.5 x (1 + erf(x / sqrt 2)), branch-free, from
+// Abramowitz & Stegun 7.1.28: erfc(z) = (1 + a1 z + ... + a6 z^6)^-16 with
+// |error| <= 3e-7. With z = |x| / sqrt 2 and R = 0.5 erfc(z) = Phi(-|x|),
+// GELU is max(x, 0) - |x| R for either sign of x. The polynomial is taken in
+// |x| (coefficient k scaled by 2^-k/2) and by 2^(1/16) overall, so its 16th
+// power is 2 / (2 R) and one reciprocal gives R: six FMAs, four squarings, a
+// reciprocal, a max and an FMA (the |x| and the sign are source modifiers).
+// Within 2.6e-7 * (1 + |x|) of the exact function; R is 0 once the power
+// overflows. The standalone GELU op and every fused epilogue use this one
+// function, so fusing a GELU changes no bit.
 __device__ __forceinline__ float gelu(float x) {
-    const float z = fabsf(x) * 0.70710678118654752440f;
-    float t = __builtin_fmaf(0.0000430638f, z, 0.0002765672f);
-    t = __builtin_fmaf(t, z, 0.0001520143f);
-    t = __builtin_fmaf(t, z, 0.0092705272f);
-    t = __builtin_fmaf(t, z, 0.0422820123f);
-    t = __builtin_fmaf(t, z, 0.0705230784f);
-    t = __builtin_fmaf(t, z, 1.0f);
+    const float ax = fabsf(x);
+    float t = __builtin_fmaf(5.621299806e-06f, ax, 5.105520904e-05f);
+    t = __builtin_fmaf(t, ax, 3.968613601e-05f);
+    t = __builtin_fmaf(t, ax, 3.422739217e-03f);
+    t = __builtin_fmaf(t, ax, 2.207699791e-02f);
+    t = __builtin_fmaf(t, ax, 5.207516253e-02f);
+    t = __builtin_fmaf(t, ax, 1.044273734e+00f);
     t = t * t;
     t = t * t;
     t = t * t;
     t = t * t;
-    const float r = __builtin_amdgcn_rcpf(t);  // erfc(z); 0 once t overflows
-    const float h = 0.5f * x;
-    return x >= 0.0f ? h * (2.0f - r) : h * r;
+    const float r = __builtin_amdgcn_rcpf(t);  // Phi(-|x|)
+    return __builtin_fmaf(-ax, r, fmaxf(x, 0.0f));
 }
 
 // The fused epilogue (kargs.h, Epilogue) for output element `idx`, after bias.

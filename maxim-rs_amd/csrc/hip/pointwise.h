@@ -139,11 +139,7 @@ __device__ void body(const GemmArgs &a) {
         }
     }
 
-    f32x4 acc[4][TMW];
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-#pragma unroll
-        for (int mt = 0; mt < TMW; ++mt) acc[j][mt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    f32x4 acc[4][TMW];  // set by the first superstep
 
     // A folded LayerNorm (CH only): this lane's four pixels' statistics for
     // the whole tile, and each superstep's scale/bias for k = 16 S + 4 g + q.
@@ -183,7 +179,9 @@ __device__ void body(const GemmArgs &a) {
             xv[q].w = (xv[q].w - lmean.w) * lrstd.w * w + c;
         }
     };
-    auto mma = [&](float4 *xv, const float4 *wv, const float4 *lv, const float4 *mv) {
+    // first: the wave's first superstep, whose multiplies start from zero
+    // (an inline-constant accumulator instead of 16 TMW register moves)
+    auto mma = [&](float4 *xv, const float4 *wv, const float4 *lv, const float4 *mv, bool first) {
         if (LN) norm(xv, lv);
         if (XMUL) {  // mx_mul's a * b
 #pragma unroll
@@ -194,16 +192,18 @@ __device__ void body(const GemmArgs &a) {
                 xv[q].w = xv[q].w * mv[q].w;
             }
         }
+        const f32x4 zero = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
         for (int t = 0; t < 4; ++t)
 #pragma unroll
             for (int j = 0; j < 4; ++j)
 #pragma unroll
                 for (int mt = 0; mt < TMW; ++mt) {
+                    const f32x4 c = first && t == 0 ? zero : acc[j][mt];
                     if (LAYOUT == CH)
-                        acc[j][mt] = mfma16(comp(xv[t], j), comp(wv[mt], t), acc[j][mt]);
+                        acc[j][mt] = mfma16(comp(xv[t], j), comp(wv[mt], t), c);
                     else
-                        acc[j][mt] = mfma16(comp(wv[mt], t), comp(xv[j], t), acc[j][mt]);
+                        acc[j][mt] = mfma16(comp(wv[mt], t), comp(xv[j], t), c);
                 }
     };
     // The bias of this lane's outputs, fetched before the reduction.
@@ -219,17 +219,19 @@ __device__ void body(const GemmArgs &a) {
     }
 
     float4 xa[4], wa[TMW], la[2], ma[4], xb[4], wb[TMW], lb[2], mb[4];
+    // Loads are unconditional (past the wave's last superstep they re-read
+    // it), so the wait before each multiply counts only the loads it needs.
     load(0, xa, wa, la, ma);
-    int s = 0;
+    load(min(1, nSw - 1), xb, wb, lb, mb);
+    mma(xa, wa, la, ma, true);
+    int s = 1;
     for (; s + 2 <= nSw; s += 2) {
-        load(s + 1, xb, wb, lb, mb);
-        mma(xa, wa, la, ma);
-        // unconditional (the last one re-reads the final superstep), so the
-        // wait before the next multiply counts only the loads it needs
-        load(min(s + 2, nSw - 1), xa, wa, la, ma);
-        mma(xb, wb, lb, mb);
+        load(s + 1, xa, wa, la, ma);
+        mma(xb, wb, lb, mb, false);
+        load(min(s + 2, nSw - 1), xb, wb, lb, mb);
+        mma(xa, wa, la, ma, false);
     }
-    if (s < nSw) mma(xa, wa, la, ma);
+    if (s < nSw) mma(xb, wb, lb, mb, false);
 
     __shared__ float red[KS == 1 ? 1 : 4 * NACC * 64];
     const int64_t cbase = (int64_t)b * a.sC;

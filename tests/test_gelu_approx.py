@@ -1,32 +1,43 @@
 """The device GELU (common.h, gelu; the standalone op and every fused
 epilogue): Abramowitz & Stegun 7.1.28 for erfc, evaluated branch-free in
-fp32. This restates its operation sequence in numpy fp32 (FMA through
-float64, one rounding) and holds it to the exact function from math.erf, so
-the approximation's error is pinned by mathematics rather than by the CPU
-path: it must stay inside the bar the GELU op is held to against the CPU
-path, |d| <= 4e-7 * (1 + |x|), including the tails where erfc underflows and
-the (1 + P)^16 power overflows."""
+fp32 as max(x, 0) - |x| Phi(-|x|), with the polynomial taken in |x| and
+scaled so that one reciprocal of its 16th power is Phi(-|x|). This restates
+its operation sequence in numpy fp32 (FMA through float64, one rounding) and
+holds it to the exact function from math.erf, so the approximation's error is
+pinned by mathematics rather than by the CPU path: it must stay inside the
+bar the GELU op is held to against the CPU path, |d| <= 4e-7 * (1 + |x|),
+including the tails where erfc underflows and the power overflows. The
+coefficients are checked against their derivation from 7.1.28's."""
 
 import math
 
 import numpy as np
 
 A6 = (0.0000430638, 0.0002765672, 0.0001520143, 0.0092705272, 0.0422820123, 0.0705230784, 1.0)
+# the device's coefficients (highest power first): a_k 2^(-k/2) 2^(1/16)
+B6 = (5.621299806e-06, 5.105520904e-05, 3.968613601e-05, 3.422739217e-03, 2.207699791e-02, 5.207516253e-02,
+      1.044273734e+00)
 
 
 def gelu_f32(x):
     f32 = np.float32
     x = x.astype(f32)
-    z = (np.abs(x) * f32(0.70710678118654752440)).astype(f32)
-    t = np.full_like(z, A6[0])
-    for c in A6[1:]:
-        t = (t.astype(np.float64) * z + f32(c)).astype(f32)
+    ax = np.abs(x)
+    t = np.full_like(ax, B6[0])
     with np.errstate(over="ignore"):
+        for c in B6[1:]:
+            t = (t.astype(np.float64) * ax + f32(c)).astype(f32)
         for _ in range(4):
             t = (t * t).astype(f32)
         r = (f32(1) / t).astype(f32)
-    h = (f32(0.5) * x).astype(f32)
-    return np.where(x >= 0, h * (f32(2) - r), h * r).astype(f32)
+    return ((-ax).astype(np.float64) * r + np.maximum(x, f32(0))).astype(f32)
+
+
+def test_coefficients_follow_7_1_28():
+    for k, (a, b) in enumerate(zip(A6, B6)):
+        power = 6 - k
+        want = np.float32(a * 2.0 ** (-power / 2.0) * 2.0 ** (1.0 / 16.0))
+        assert np.float32(b) == want, (k, b, want)
 
 
 def test_gelu_fused_error_bound():
@@ -37,5 +48,5 @@ def test_gelu_fused_error_bound():
     err = np.abs(got - exact) / (1.0 + np.abs(x.astype(np.float64)))
     assert np.isfinite(got).all()
     assert err.max() <= 4e-7, (err.max(), x[err.argmax()])
-    # the known worst region of 7.1.28 sits near z = 2.85 (x = 4.03)
+    # an approximation (worst near x = -0.79), not the exact function
     assert err.max() > 1e-8
