@@ -483,7 +483,7 @@ private:
     // when its shape and alignment allow them; `layout` 0 = channel-major
     // output, 1 = row-major. `alt` keeps the tiled-GEMM launch of each op that
     // got one, for fused steps whose extra operands are not 16-byte aligned.
-    bool try_pw(int layout, const GemmArgs &a, Launch &l) {
+    bool try_pw(int layout, const GemmArgs &a, Launch &l, bool whole = false) {
         if (no_pw) return false;
         const int64_t wout = layout == 0 ? a.M : a.N, slen = layout == 0 ? a.N : a.M;
         if (a.K % 16 || a.N % 4 || a.K == 0 || wout <= 0 || slen <= 0) return false;
@@ -503,7 +503,10 @@ private:
         const int64_t nib = (wout + 16 * tmw - 1) / (16 * tmw);
         const int64_t tiles = nib * ((slen + 63) / 64);
         if (tiles > 0x7fffffffLL) return false;
-        const bool k4 = a.K % 64 == 0 && (a.K >= 128 || tiles * a.batch < 2LL * 4 * cus);
+        // whole: the reduction stays in one wave (a step whose epilogue
+        // normalises bands across several waves of a block, which needs them
+        // to hold whole tiles)
+        const bool k4 = !whole && a.K % 64 == 0 && (a.K >= 128 || tiles * a.batch < 2LL * 4 * cus);
         l = mk(std::string(names[layout][ti]) + (k4 ? "_k4" : ""));
         const int64_t grid = k4 ? tiles : (tiles + 3) / 4;
         if (grid > 0x7fffffffLL) return false;
@@ -514,6 +517,7 @@ private:
         return true;
     }
     std::vector<std::vector<Launch>> alt;
+    std::vector<char> whole_k;  // per op: keep a streaming GEMM's reduction in one wave
     bool no_pw = getenv("MAXIM_NO_PW") != nullptr;
     void validate(const mx_plan_desc *p) const;
     void build_launches(const mx_plan_desc *p, const std::vector<int64_t> &woff,
@@ -769,6 +773,24 @@ Gpu::Gpu(const mx_plan_desc *p) : H(hip()), doff(pg.doff) {
     pg.plan_fusion(p, !repack);
     pg.layout(p, repack);
     arena_len = pg.arena_len;
+    // A 1x1 conv whose step normalises (or takes the statistics of) output
+    // bands of 128 channels needs whole tiles per wave, so four waves of a
+    // block hold a band (64-channel bands fit one 64-wide wave with the
+    // split reduction). Up to 128 inputs, with at least two 32-wide tiles per
+    // SIMD, that costs the split reduction 1-2 us (measured at the MAXIM
+    // 112x160 shapes) and saves a LayerNorm or statistics pass; with fewer
+    // tiles (56x80) the whole reductions cost more than the pass. Its own
+    // launch takes the same form, so the fused and unfused passes still
+    // agree to the bit.
+    whole_k.assign(p->n_ops, 0);
+    for (const StepSpec &sp : pg.specs) {
+        const uint64_t g = sp.ln >= 0 ? sp.first + 1 : sp.first;
+        if (g >= p->n_ops || p->ops[g].kind != MX_OP_CONV1X1 || p->ops[g].c_in > 128) continue;
+        const mx_op &c = p->ops[g];
+        const int64_t band = sp.lno >= 0 ? p->ops[sp.lno].c : sp.so_nband > 0 ? sp.so_c : 0;
+        const int64_t tiles = (c.c_out + 31) / 32 * ((c.h * c.wd + 63) / 64);
+        if (band > 64 && tiles >= 8LL * cus) whole_k[g] = 1;
+    }
 
     // Size the pass before allocating it, and refuse with the numbers.
     wbytes = blob.size() * 4;
@@ -931,7 +953,7 @@ void Gpu::build_launches(const mx_plan_desc *p, const std::vector<int64_t> &woff
                 set_args(l, a);
                 l.kind = 1;
                 Launch q;
-                if (try_pw(0, a, q)) {
+                if (try_pw(0, a, q, whole_k[i])) {
                     alt[i].push_back(l);
                     L.push_back(q);
                 } else {
