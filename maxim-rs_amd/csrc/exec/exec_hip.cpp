@@ -1472,6 +1472,20 @@ void Program::plan_fusion(const mx_plan_desc *p, bool require_clear) {
                     sp.r1 = r;
                     sp.out = n1.dst;
                     sp.last = i + 2;
+                    // and a second Add of that sum (a block's long skip), read by nothing else
+                    if (i + 2 < p->n_ops) {
+                        const mx_op &n2 = p->ops[i + 2];
+                        const int64_t y = n1.dst;
+                        if (n2.kind == MX_OP_ADD && (n2.src == y) != (n2.src2 == y) && whole(n2, y) &&
+                            only_reader(y, i + 1, i + 2)) {
+                            const int64_t r2 = n2.src == y ? n2.src2 : n2.src;
+                            if (clear_of(n2.dst, {o.src, o.src2, r, r2, y})) {
+                                sp.r2 = r2;
+                                sp.out = n2.dst;
+                                sp.last = i + 3;
+                            }
+                        }
+                    }
                 }
             }
         }
@@ -2068,7 +2082,9 @@ void Gpu::build_program(const mx_plan_desc *p) {
             memcpy(&a, ops[sp.first][0].a0, sizeof a);
             a.y = dev(sp.out);
             a.r = dev(sp.r1);
-            const bool vec = a.hw % 4 == 0 && aligned(a.x, 16) && aligned(a.y, 16) && aligned(a.r, 16);
+            a.r2 = dev(sp.r2);
+            const bool vec = a.hw % 4 == 0 && aligned(a.x, 16) && aligned(a.y, 16) && aligned(a.r, 16) &&
+                             aligned(a.r2, 16);
             Launch l = mk(vec ? "mx_chan_scale_add_v4" : "mx_chan_scale_add_s");
             l.g[0] = vec ? cdiv(a.hw / 4, MXK_BLOCK * 4) : cdiv(a.hw, MXK_BLOCK);
             l.g[1] = grid_yz(a.c);

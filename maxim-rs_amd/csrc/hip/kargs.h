@@ -21,7 +21,7 @@ struct EwArgs {
 };
 
 // y[ch][p] = x[ch][p] * s[ch] (+ r[ch][p] when r is set: a residual add
-// fused into the scale)
+// fused into the scale; then + r2[ch][p] when r2 is set: a second add)
 struct ChanScaleArgs {
     const float *x;
     const float *s;
@@ -29,6 +29,7 @@ struct ChanScaleArgs {
     int64_t hw;
     int64_t c;
     const float *r;
+    const float *r2;
 };
 
 // The channel-attention MLP on a [c] vector, one block:

@@ -99,21 +99,23 @@ extern "C" __global__ __launch_bounds__(MXK_BLOCK) void mx_chan_scale_s(ChanScal
 }
 
 // The CALayer's excitation and the residual add as one pass:
-// y = x * s[ch] + r, the two unfused kernels' operations in their order.
+// y = x * s[ch] + r (+ r2), the unfused kernels' operations in their order.
 extern "C" __global__ __launch_bounds__(MXK_BLOCK) void mx_chan_scale_add_v4(ChanScaleArgs a) {
     const int64_t ch = blockIdx.y;
     const float s = a.s[ch];
     const float *x = a.x + ch * a.hw;
     const float *r = a.r + ch * a.hw;
+    const float *r2 = a.r2 ? a.r2 + ch * a.hw : nullptr;
     float *y = a.y + ch * a.hw;
     const int64_t nv = a.hw >> 2;
-    float4 v[4], w[4];
+    float4 v[4], w[4], w2[4];
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
         const int64_t j = (int64_t)blockIdx.x * (MXK_BLOCK * 4) + u * MXK_BLOCK + threadIdx.x;
         if (j < nv) {
             v[u] = ld4(x + 4 * j);
             w[u] = ld4(r + 4 * j);
+            if (r2) w2[u] = ld4(r2 + 4 * j);
         }
     }
 #pragma unroll
@@ -125,6 +127,12 @@ extern "C" __global__ __launch_bounds__(MXK_BLOCK) void mx_chan_scale_add_v4(Cha
             t.y = t.y * s + w[u].y;
             t.z = t.z * s + w[u].z;
             t.w = t.w * s + w[u].w;
+            if (r2) {
+                t.x = t.x + w2[u].x;
+                t.y = t.y + w2[u].y;
+                t.z = t.z + w2[u].z;
+                t.w = t.w + w2[u].w;
+            }
             st4(y + 4 * j, t);
         }
     }
@@ -135,7 +143,9 @@ extern "C" __global__ __launch_bounds__(MXK_BLOCK) void mx_chan_scale_add_s(Chan
     int64_t p = (int64_t)blockIdx.x * MXK_BLOCK + threadIdx.x;
     if (p < a.hw) {
         const int64_t i = ch * a.hw + p;
-        a.y[i] = a.x[i] * a.s[ch] + a.r[i];
+        float v = a.x[i] * a.s[ch] + a.r[i];
+        if (a.r2) v = v + a.r2[i];
+        a.y[i] = v;
     }
 }
 

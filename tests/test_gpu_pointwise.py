@@ -548,3 +548,35 @@ def test_layernorm_statistics_from_the_producer(gpu_ok, c, k, h, w):
     err = float(np.abs(got.astype(np.float64) - want).max())
     print("max-abs vs CPU %.3g (max|cpu| %.3g)" % (err, float(np.abs(want).max())))
     assert err <= 1e-3, err
+
+
+@pytest.mark.parametrize("c,h,w,second", [
+    (32, 16, 40, True),    # the RCAB output, then a block's long skip: one pass
+    (64, 9, 20, False),    # ChanScale -> Add only
+    (16, 5, 7, True),      # 35 pixels: the scalar kernel
+])
+def test_channel_scale_with_residual_adds(gpu_ok, c, h, w, second):
+    """ChanScale -> Add [-> Add] (src/exec_cpu.rs chan_scale and add): one
+    pass that scales, adds the residual and then the second operand in the
+    unfused order; bit-exact against the CPU path and the unfused pass."""
+    from maxim_amd import plan as P
+    from maxim_amd import hip as H
+    rng = np.random.default_rng(c * 31 + h * w)
+    hw = h * w
+    X, S, T, R, Y, R2, Z = range(7)
+    bufs = [(c, h, w), (c, 1, 1), (c, h, w), (c, h, w), (c, h, w), (c, h, w), (c, h, w)]
+    ops = [P.make_op(P.CHAN_SCALE, dst=T, src=X, src2=S, c=c, hw=hw),
+           P.make_op(P.ADD, dst=Y, src=R, src2=T, n=c * hw)]
+    if second:
+        ops.append(P.make_op(P.ADD, dst=Z, src=Y, src2=R2, n=c * hw))
+    out = Z if second else Y
+    cp = P.CustomPlan(bufs, ops, [], input=X, output=out)
+    inputs = {X: rng.standard_normal(bufs[X]).astype(np.float32),
+              S: rng.standard_normal(bufs[S]).astype(np.float32),
+              R: rng.standard_normal(bufs[R]).astype(np.float32),
+              R2: rng.standard_normal(bufs[R2]).astype(np.float32)}
+    got, steps = run_plan(cp, inputs, out)
+    print("steps", steps)
+    assert len(steps) == 1 and steps[0][2].startswith("mx_chan_scale_add"), steps
+    want = oracle_plan(cp, inputs, out)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
