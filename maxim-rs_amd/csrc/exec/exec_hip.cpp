@@ -14,6 +14,7 @@
 #include <cmath>
 #include <cstdlib>
 #include <cstring>
+#include <functional>
 #include <map>
 #include <memory>
 #include <set>
@@ -1355,10 +1356,12 @@ void Program::plan_fusion(const mx_plan_desc *p, bool require_clear) {
     };
 
     // Copy elision (own device layout only): a copy whose source x has one
-    // writer, and whose destination's bytes nothing touches between that
-    // writer and the copy nor rewrites while x is still read after it, is
-    // served by laying x out on the destination's storage: the writer then
-    // produces the destination directly (x's other readers, e.g. a skip
+    // writer (or is written only through the views inside it, slot by slot:
+    // a concatenation copied whole into a larger one), and whose
+    // destination's bytes nothing touches between x's first write and the
+    // copy nor rewrites while x is still read after it, is served by laying
+    // x (and its views) out on the destination's storage: the writers then
+    // produce the destination directly (x's other readers, e.g. a skip
     // connection's, read it there) and the copy's step launches nothing (run
     // op by op it copies the destination onto itself). Checked per storage
     // owner (the view table's base), since the executor lays out every owner
@@ -1390,29 +1393,40 @@ void Program::plan_fusion(const mx_plan_desc *p, bool require_clear) {
                 if (shares(b, d)) return true;
             return false;
         };
+        // x's family: x and the views inside it (a concatenation written
+        // slot by slot through its views)
+        auto in_x = [&](int64_t b, int64_t x) { return b >= 0 && base[b] == x; };
         for (uint64_t j = 0; j < p->n_ops; ++j) {
             const mx_op &c = p->ops[j];
             if (c.kind != MX_OP_COPY) continue;
             const int64_t x = c.src, d = c.dst;
-            if (x == d || base[x] != x || views[x] || writers[x] != 1 || target[x] || elide_to[d] >= 0 ||
-                elide_to[x] >= 0)  // x copied twice: it takes the first destination only
+            if (x == d || base[x] != x || (!views[x] && writers[x] != 1) || (views[x] && writers[x]) || target[x] ||
+                elide_to[d] >= 0 || elide_to[x] >= 0)  // x copied twice: it takes the first destination only
                 continue;
             if ((uint64_t)x == p->input || (uint64_t)x == p->output || (p->keep && p->keep[x])) continue;
             if ((uint64_t)c.n != blen(x) || (uint64_t)c.n != blen(d)) continue;
-            int64_t w = -1;  // x's writer
-            for (uint64_t k = 0; k < j; ++k)
-                for (int64_t b : writes_of(p->ops[k]))
-                    if (b == x) w = (int64_t)k;
-            if (w < 0) continue;
             bool ok = true;
+            // w: x's writer, or the first writer of one of its views; every
+            // writer of the family before the copy reads no byte of d
+            int64_t w = -1;
+            for (uint64_t k = 0; k < j && ok; ++k)
+                for (int64_t b : writes_of(p->ops[k]))
+                    if (in_x(b, x)) {
+                        if (views[x]) {
+                            if (w < 0) w = (int64_t)k;
+                        } else {
+                            w = (int64_t)k;
+                        }
+                        for (int64_t r : reads_of(p->ops[k])) ok = ok && !shares(r, d);
+                    }
+            if (w < 0 || !ok) continue;
             uint64_t last_read = j;  // x's last reader (x may have others: a skip connection)
             for (uint64_t k = 0; k < p->n_ops; ++k)
                 for (int64_t b : reads_of(p->ops[k]))
-                    if (b == x) {
+                    if (in_x(b, x)) {
                         if (k < (uint64_t)w) ok = false;  // nothing reads x before it is written
                         last_read = std::max(last_read, k);
                     }
-            for (int64_t b : reads_of(p->ops[w])) ok = ok && !shares(b, d);  // the writer reads no byte of d
             for (uint64_t k = (uint64_t)w + 1; k < j && ok; ++k) ok = !touches(p->ops[k], d);
             // d's bytes keep x's value for as long as x is read after the copy
             for (uint64_t k = j + 1; k <= last_read && ok; ++k)
@@ -1778,12 +1792,22 @@ void Program::layout(const mx_plan_desc *p, bool repack) {
             delta[i] = delta[par] + p->alias_delta[i];
         }
     }
-    // an elided copy's source takes its destination's storage
-    for (uint64_t i = 0; i < n; ++i)
-        if (i < elide_to.size() && elide_to[i] >= 0) {
-            base[i] = base[elide_to[i]];
-            delta[i] = delta[elide_to[i]];
+    // an elided copy's source (with the views inside it) takes its
+    // destination's storage, which may itself sit on another's
+    std::vector<char> done(n, 0);
+    std::function<void(uint64_t)> resolve = [&](uint64_t i) {
+        if (done[i]) return;
+        done[i] = 1;
+        const int64_t x = base[i];
+        if (x < (int64_t)elide_to.size() && elide_to[x] >= 0) {
+            const int64_t d = elide_to[x];
+            resolve((uint64_t)d);
+            const uint64_t dx = delta[i];  // offset inside x
+            base[i] = base[d];
+            delta[i] = delta[d] + dx;
         }
+    };
+    for (uint64_t i = 0; i < n; ++i) resolve(i);
     for (uint64_t i = 0; i < n; ++i) dbase[i] = base[i];
     const uint64_t DEAD = UINT64_MAX;
     std::vector<uint64_t> first(n, DEAD), last(n, 0);
