@@ -33,7 +33,7 @@ __device__ void body(const ConvArgs &a) {
     constexpr int NH = (HALO + 255) / 256;          // halo elements per thread
     constexpr int LDS = WTN + 4;  // row pitch of a wave's output staging tile
     constexpr int POOL = KC * LDM + HALO > 4 * 16 * LDS ? KC * LDM + HALO : 4 * 16 * LDS;
-    static_assert(KC % 4 == 0 && BM % 16 == 0 && TW % 4 == 0, "tile");
+    static_assert(KC % 4 == 0 && CK % 4 == 0 && BM % 16 == 0 && TW % 4 == 0, "tile");
     static_assert(WAVES_M * WAVES_N == 4 && TM >= 1 && TN >= 1, "wave grid");
     __shared__ float smem[POOL];
     float (*Ws)[LDM] = reinterpret_cast<float (*)[LDM]>(smem);
@@ -82,6 +82,15 @@ __device__ void body(const ConvArgs &a) {
         }
     };
 
+    // This lane's LDS read bases: its k row of the weight tile (k = kk + lk)
+    // and its channel plane of the halo at each of its B columns; every step
+    // of the reduction adds a constant to them, so the fully unrolled loop
+    // below addresses LDS through instruction offsets alone.
+    const float *wl = &Ws[lk][wm * WTM + lr];
+    const float *hl[TN];
+#pragma unroll
+    for (int j = 0; j < TN; ++j) hl[j] = Hs + lk * (HH * HW) + nofs[j];
+
     f32x4 acc[TM][TN];
 #pragma unroll
     for (int i = 0; i < TM; ++i)
@@ -103,16 +112,15 @@ __device__ void body(const ConvArgs &a) {
         }
         __syncthreads();
         if (chunk + 1 < nchunk) fetch(chunk + 1);
-#pragma unroll 2
+        // k = kk + lk: tap kk / CK (CK % 4 == 0), channel kk % CK + lk
+#pragma unroll
         for (int kk = 0; kk < KC; kk += 4) {
-            const int k = kk + lk;
-            const int tap = k / CK, c = k % CK;
-            const float *hb = &Hs[c * (HH * HW) + (tap / KS) * HW + (tap % KS)];
+            const int tap = kk / CK, hofs = (kk % CK) * (HH * HW) + (tap / KS) * HW + (tap % KS);
             float af[TM], bf[TN];
 #pragma unroll
-            for (int i = 0; i < TM; ++i) af[i] = Ws[k][wm * WTM + i * 16 + lr];
+            for (int i = 0; i < TM; ++i) af[i] = wl[kk * LDM + i * 16];
 #pragma unroll
-            for (int j = 0; j < TN; ++j) bf[j] = hb[nofs[j]];
+            for (int j = 0; j < TN; ++j) bf[j] = hl[j][hofs];
 #pragma unroll
             for (int i = 0; i < TM; ++i)
 #pragma unroll
