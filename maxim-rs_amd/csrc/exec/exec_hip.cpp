@@ -50,6 +50,7 @@ struct Launch {
 // A run of ops [first, last) executed by `launches`: one op's own launches,
 // or one fused launch standing for several ops.
 struct Step {
+    Step(uint64_t f, uint64_t l, std::vector<Launch> v = {}) : first(f), last(l), launches(std::move(v)) {}
     uint64_t first, last;
     std::vector<Launch> launches;
     size_t main = 0;  // the launch that names the step in reports
@@ -882,7 +883,7 @@ void Gpu::build_launches(const mx_plan_desc *p, const std::vector<int64_t> &woff
                 break;
             }
             case MX_OP_CHAN_SCALE: {
-                ChanScaleArgs a{B(o.src), B(o.src2), B(o.dst), o.hw, o.c, nullptr};
+                ChanScaleArgs a{B(o.src), B(o.src2), B(o.dst), o.hw, o.c, nullptr, nullptr};
                 bool vec = o.hw % 4 == 0 && aligned(a.x, 16) && aligned(a.y, 16);
                 Launch l = mk(vec ? "mx_chan_scale_v4" : "mx_chan_scale_s");
                 l.g[0] = vec ? cdiv(o.hw / 4, MXK_BLOCK * 4) : cdiv(o.hw, MXK_BLOCK);
