@@ -1155,7 +1155,8 @@ void Gpu::build_launches(const mx_plan_desc *p, const std::vector<int64_t> &woff
                         Resize2Args r{B(o.src), B(o.dst), X(i, 0), X(i, 1), (int32_t)o.h, (int32_t)o.wd,
                                       (int32_t)o.oh, (int32_t)o.ow, maxt[i][0], maxt[i][1], (int32_t)pick,
                                       (int32_t)tiles_x, pick_band, span};
-                        Launch l = mk(tw == 256 ? "mx_resize_hv4" : "mx_resize_hv");
+                        const int mt = std::max(maxt[i][0], maxt[i][1]), ut = mt <= 2 ? 2 : mt <= 4 ? 4 : 8;
+                        Launch l = mk(std::string(tw == 256 ? "mx_resize_hv4_t" : "mx_resize_hv_t") + std::to_string(ut));
                         l.g[0] = (uint32_t)(tiles_x * cdiv(o.oh, pick));
                         l.g[1] = (uint32_t)o.c;
                         l.shm = (unsigned)(4 * (pick_band * (span + tw) + pick * (3 + mv)));

@@ -519,8 +519,13 @@ __device__ __forceinline__ float rs_norm(float acc, float ws) {
     return ws > 0.0f && ws != 1.0f ? acc / ws : acc;
 }
 
-template <int TW>
+// MT: taps per table row the loops are unrolled for (>= the tables' own,
+// which the host picks it from: 2 for bilinear upsampling, 4 or 8 for the
+// antialiased downsampling), so an upsampling kernel carries no predicated
+// dead taps.
+template <int TW, int MT>
 __device__ void resize_hv(const Resize2Args &a) {
+    static_assert(MT <= RS_MAXT, "taps");
     extern __shared__ float rs_lds[];
     float *in = rs_lds;                               // [band][span]
     float *tmp = rs_lds + a.band * a.span;            // [band][TW]
@@ -537,10 +542,26 @@ __device__ void resize_hv(const Resize2Args &a) {
     const int jlo = (int)vf[0], nr = (int)vl[0] + (int)vl[1] - jlo;
     const int xlo = (int)hf[0], xn = (int)hl[0] + (int)hl[1] - xlo;
     for (int q = tid; q < nrow * sv; q += 256) vt[q] = vf[q];
+    // the input rows and columns this block reads, eight loads in flight per
+    // thread before any of them is written to LDS
     const float *src = a.x + ((int64_t)ch * a.h + jlo) * a.wd + xlo;
-    for (int q = tid; q < nr * xn; q += 256) {
-        const int r = q / xn, c = q - r * xn;
-        in[r * a.span + c] = src[(int64_t)r * a.wd + c];
+    const int total = nr * xn;
+    for (int q0 = tid; q0 < total; q0 += 8 * 256) {
+        float v[8];
+        int at[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const int q = q0 + u * 256;
+            at[u] = -1;
+            if (q < total) {
+                const int r = q / xn, c = q - r * xn;
+                v[u] = src[(int64_t)r * a.wd + c];
+                at[u] = r * a.span + c;
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u)
+            if (at[u] >= 0) in[at[u]] = v[u];
     }
     __syncthreads();
 
@@ -551,15 +572,15 @@ __device__ void resize_hv(const Resize2Args &a) {
         const float *e = a.th + (int64_t)(ox0 + col) * sh;
         const int b = (int)e[0] - xlo, nt = (int)e[1];
         const float ws = e[2];
-        float w[RS_MAXT];
+        float w[MT];
 #pragma unroll
-        for (int k = 0; k < RS_MAXT; ++k) w[k] = k < a.mth ? e[3 + k] : 0.0f;
+        for (int k = 0; k < MT; ++k) w[k] = k < a.mth ? e[3 + k] : 0.0f;
         const int r0 = TW == 256 ? 0 : wave, dr = TW == 256 ? 1 : 4;
         for (int r = r0; r < nr; r += dr) {
             const float *sr = in + r * a.span + b;
             float acc = 0.0f;
 #pragma unroll
-            for (int k = 0; k < RS_MAXT; ++k)
+            for (int k = 0; k < MT; ++k)
                 if (k < nt) acc += w[k] * sr[k];
             tmp[r * TW + col] = rs_norm(acc, ws);
         }
@@ -577,7 +598,7 @@ __device__ void resize_hv(const Resize2Args &a) {
             const float vs = e[2];
             float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-            for (int k = 0; k < RS_MAXT; ++k)
+            for (int k = 0; k < MT; ++k)
                 if (k < n) {
                     const float wk = e[3 + k];
                     const float4 t = ld4(tmp + (b + k) * TW + c0);
@@ -607,12 +628,18 @@ __device__ void resize_hv(const Resize2Args &a) {
             const float *t = tmp + b * TW + lane;
             float acc = 0.0f;
 #pragma unroll
-            for (int k = 0; k < RS_MAXT; ++k)
+            for (int k = 0; k < MT; ++k)
                 if (k < n) acc += e[3 + k] * t[k * TW];
             yrow[(int64_t)r * a.ow + lane] = rs_norm(acc, vs);
         }
     }
 }
 
-extern "C" __global__ __launch_bounds__(256) void mx_resize_hv(Resize2Args a) { resize_hv<64>(a); }
-extern "C" __global__ __launch_bounds__(256) void mx_resize_hv4(Resize2Args a) { resize_hv<256>(a); }
+// mx_resize_hv[4]_t<MT>: 64 (256) output columns per block, tables of at
+// most MT taps.
+#define MXK_RS(MT)                                                                                  \
+    extern "C" __global__ __launch_bounds__(256) void mx_resize_hv_t##MT(Resize2Args a) { resize_hv<64, MT>(a); } \
+    extern "C" __global__ __launch_bounds__(256) void mx_resize_hv4_t##MT(Resize2Args a) { resize_hv<256, MT>(a); }
+MXK_RS(2)
+MXK_RS(4)
+MXK_RS(8)
