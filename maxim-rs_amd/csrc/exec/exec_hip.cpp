@@ -1703,12 +1703,22 @@ void Program::plan_fusion(const mx_plan_desc *p, bool require_clear) {
                         if (overlap(range(d), xr)) P = s2;
             if (P < 0) continue;
             const StepSpec &S = specs[P];
-            if (S.rule != RULE_NONE || S.lno >= 0 || S.xmul >= 0 || S.xperm >= 0) continue;
-            const uint64_t g = S.ln >= 0 ? S.first + 1 : S.first;
-            const mx_op &c = p->ops[g];
-            if (c.kind != MX_OP_CONV1X1 || c.h * c.wd <= 1) continue;
-            const int64_t y = S.out >= 0 ? S.out : c.dst;
-            const uint64_t hw = (uint64_t)(c.h * c.wd);
+            int64_t y = -1;
+            uint64_t hw = 0;
+            if (S.rule == RULE_SCALE_ADD) {
+                // the CALayer's scaled residual sum, the whole buffer one band
+                const mx_op &c = p->ops[S.first];
+                y = S.out;
+                hw = (uint64_t)c.hw;
+                if (ln.c != c.c) continue;
+            } else {
+                if (S.rule != RULE_NONE || S.lno >= 0 || S.xmul >= 0 || S.xperm >= 0) continue;
+                const uint64_t g = S.ln >= 0 ? S.first + 1 : S.first;
+                const mx_op &c = p->ops[g];
+                if (c.kind != MX_OP_CONV1X1 || c.h * c.wd <= 1) continue;
+                y = S.out >= 0 ? S.out : c.dst;
+                hw = (uint64_t)(c.h * c.wd);
+            }
             const R yr = range(y);
             if (ln.hw != (int64_t)hw || xr.a < yr.a || xr.b > yr.b || (xr.a - yr.a) % hw ||
                 xr.b - xr.a != (uint64_t)ln.c * hw)
@@ -2111,6 +2121,18 @@ void Gpu::build_program(const mx_plan_desc *p) {
             a.r2 = dev(sp.r2);
             const bool vec = a.hw % 4 == 0 && aligned(a.x, 16) && aligned(a.y, 16) && aligned(a.r, 16) &&
                              aligned(a.r2, 16);
+            if (sp.so_nband == 1 && vec && (a.c == 32 || a.c == 64 || a.c == 128)) {
+                // with the statistics of the sum for a later folded LayerNorm
+                ScaleAddLnArgs b{a.x, a.s, a.r, a.r2, a.y, scratch + so_base + sp.so_out, a.hw, (int32_t)a.c,
+                                 mx::kEps};
+                const auto t = ln_tile(a.c, a.hw, cus);
+                Launch l = mk("mx_chan_scale_add_stats_c" + std::to_string(a.c) + t.second);
+                l.g[0] = cdiv(a.hw, t.first);
+                set_args(l, b);
+                so_ok[&sp - pg.specs.data()] = 1;
+                prog.push_back(Step{sp.first, sp.last, {l}});
+                continue;
+            }
             Launch l = mk(vec ? "mx_chan_scale_add_v4" : "mx_chan_scale_add_s");
             l.g[0] = vec ? cdiv(a.hw / 4, MXK_BLOCK * 4) : cdiv(a.hw, MXK_BLOCK);
             l.g[1] = grid_yz(a.c);

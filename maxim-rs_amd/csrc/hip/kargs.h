@@ -53,6 +53,17 @@ struct CaMeanArgs {
     int32_t nchunk, pad;
 };
 
+// ChanScale -> Add [-> Add] as mx_chan_scale_add computes it (y = x * s[ch]
+// + r (+ r2)), with the per-pixel LayerNorm statistics of y ([2][hw]: mean,
+// then 1 / std) for a LayerNorm folded into a later GEMM.
+struct ScaleAddLnArgs {
+    const float *x, *s, *r, *r2;
+    float *y, *stats;
+    int64_t hw;
+    int32_t c;
+    float eps;
+};
+
 // Channel LayerNorm over [c][hw].
 struct ChanLnArgs {
     const float *x;

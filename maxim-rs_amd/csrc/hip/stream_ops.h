@@ -273,6 +273,69 @@ __device__ void chan_ln_tile(const ChanLnArgs &a) {
     }
 }
 
+// The CALayer's excitation and residual add(s), as mx_chan_scale_add_v4
+// computes them, with the LayerNorm statistics of the result in
+// chan_ln_tile's order and expression: the same LDS tile, filled with the
+// sums it stores.
+template <int C, int P>
+__device__ void scale_add_stats_tile(const ScaleAddLnArgs &a) {
+    static_assert(C * P <= 8192 && P % 4 == 0 && P <= MXK_BLOCK, "a tile of at most 32 KiB");
+    __shared__ float t[C][P];
+    const int tid = threadIdx.x;
+    const int64_t p0 = (int64_t)blockIdx.x * P;
+    const bool full = p0 + P <= a.hw;
+    constexpr int Q = P / 4;
+    for (int i = tid; i < C * Q; i += MXK_BLOCK) {
+        const int c = i / Q, q = (i % Q) * 4;
+        const int64_t off = (int64_t)c * a.hw + p0 + q;
+        const float s = a.s[c];
+        float4 v;
+        if (full) {
+            v = ld4(a.x + off);
+            const float4 w = ld4(a.r + off);
+            v.x = v.x * s + w.x;
+            v.y = v.y * s + w.y;
+            v.z = v.z * s + w.z;
+            v.w = v.w * s + w.w;
+            if (a.r2) {
+                const float4 w2 = ld4(a.r2 + off);
+                v.x = v.x + w2.x;
+                v.y = v.y + w2.y;
+                v.z = v.z + w2.z;
+                v.w = v.w + w2.w;
+            }
+            st4(a.y + off, v);
+        } else {
+            float e[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int u = 0; u < 4; ++u)
+                if (p0 + q + u < a.hw) {
+                    float y = a.x[off + u] * s + a.r[off + u];
+                    if (a.r2) y = y + a.r2[off + u];
+                    a.y[off + u] = y;
+                    e[u] = y;
+                }
+            v = make_float4(e[0], e[1], e[2], e[3]);
+        }
+        st4(&t[c][q], v);
+    }
+    __syncthreads();
+    if (tid < P && p0 + tid < a.hw) {
+        float s1 = 0.0f, s2 = 0.0f;
+#pragma unroll 8
+        for (int c = 0; c < C; ++c) {
+            const float v = t[c][tid];
+            s1 += v;
+            s2 += v * v;
+        }
+        const float nf = (float)C;
+        const float m = s1 / nf;
+        const float var = s2 / nf - m * m;
+        a.stats[p0 + tid] = m;
+        a.stats[a.hw + p0 + tid] = 1.0f / sqrtf(fmaxf(var, 0.0f) + a.eps);
+    }
+}
+
 // 128-bit paths need hw % 4 == 0 and 16-byte aligned x and y.
 // mx_chan_ln_c<C>[_p<P>] and mx_chan_ln_stats_c<C>[_p<P>]: C channels x P
 // pixels per block (P = 8192 / C without the suffix); the smaller tiles give
@@ -284,6 +347,9 @@ __device__ void chan_ln_tile(const ChanLnArgs &a) {
     }                                                                                               \
     extern "C" __global__ __launch_bounds__(MXK_BLOCK) void mx_chan_ln_stats_c##C##SUF(ChanLnArgs a) { \
         chan_ln_tile<C, P, true>(a);                                                                \
+    }                                                                                               \
+    extern "C" __global__ __launch_bounds__(MXK_BLOCK) void mx_chan_scale_add_stats_c##C##SUF(ScaleAddLnArgs a) { \
+        scale_add_stats_tile<C, P>(a);                                                              \
     }
 MXK_LN(32, 256, )
 MXK_LN(32, 128, _p128)

@@ -62,9 +62,9 @@ def test_the_code_object_is_embedded_and_complete():
     launched |= {"mx_pw_ch%d%s%s_f_lo" % (t, k, l) for t in (2, 4) for k in ("", "_k4") for l in ("", "_ln")}
     launched |= {"mx_c3_m%d_t%d%s" % (m, t, f) for m, t in ((32, 8), (64, 4), (64, 2)) for f in ("", "_f")}
     launched |= {"mx_resize_hv%s_t%d" % (v, t) for v in ("", "4") for t in (2, 4, 8)}
-    launched |= {"mx_chan_ln%s_c%d%s" % (s, c, p) for s in ("", "_stats") for c in (32, 64, 128)
-                 for p in ("", "_p%d" % (4096 // c), "_p%d" % (2048 // c))}
-    launched = {k for k in launched if not k.endswith("_")}
+    launched |= {"mx_chan%s_c%d%s" % (s, c, p) for s in ("_ln", "_ln_stats", "_scale_add_stats")
+                 for c in (32, 64, 128) for p in ("", "_p%d" % (4096 // c), "_p%d" % (2048 // c))}
+    launched = {k for k in launched if not k.endswith("_") and not k.endswith("_c")}
     missing = [k for k in sorted(launched) if k.encode() + b"\0" not in data]
     assert not missing, missing
 

@@ -580,3 +580,68 @@ def test_channel_scale_with_residual_adds(gpu_ok, c, h, w, second):
     assert len(steps) == 1 and steps[0][2].startswith("mx_chan_scale_add"), steps
     want = oracle_plan(cp, inputs, out)
     assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+@pytest.mark.parametrize("c,h,w", [
+    (64, 16, 40),     # whole tiles
+    (128, 14, 20),    # 280 pixels: a partial last tile
+    (32, 9, 20),
+])
+def test_layernorm_statistics_from_the_channel_scale(gpu_ok, c, h, w):
+    """ChanScale -> Add -> Add (an RCAB's output plus a block's skip), then
+    the sum LayerNormed into a 1x1 conv after an unrelated reader: the
+    scale-add pass writes the sum's statistics and the folded GEMM reads
+    them (no statistics pass). Bitwise the unfused pass, also for a run of
+    ops that starts after the producer; the CPU path to the GEMM bar."""
+    from maxim_amd import plan as P
+    from maxim_amd import hip as H
+    rng = np.random.default_rng(c * 13 + h * w)
+    hw = h * w
+    X, S, T, R, Y, R2, Z, A, ZN, O, OUT = range(11)
+    bufs = [(c, h, w), (c, 1, 1), (c, h, w), (c, h, w), (c, h, w), (c, h, w), (c, h, w), (c, h, w),
+            (c, h, w), (c, h, w), (c, h, w)]
+    wts = [he(rng, (c, c), c), (rng.standard_normal(c) * 0.1).astype(np.float32),
+           (1 + 0.1 * rng.standard_normal(c)).astype(np.float32), (0.1 * rng.standard_normal(c)).astype(np.float32)]
+    ops = [P.make_op(P.CHAN_SCALE, dst=T, src=X, src2=S, c=c, hw=hw),
+           P.make_op(P.ADD, dst=Y, src=R, src2=T, n=c * hw),
+           P.make_op(P.ADD, dst=Z, src=Y, src2=R2, n=c * hw),
+           P.make_op(P.ADD, dst=A, src=Z, src2=R, n=c * hw),          # another reader in between
+           P.make_op(P.CHAN_LN, dst=ZN, src=Z, scale=2, bias=3, c=c, hw=hw),
+           P.make_op(P.CONV1X1, dst=O, src=ZN, w=0, bias=1, c_in=c, c_out=c, h=h, wd=w),
+           P.make_op(P.ADD, dst=OUT, src=O, src2=A, n=c * hw)]
+    cp = P.CustomPlan(bufs, ops, wts, input=X, output=OUT)
+    inputs = {X: rng.standard_normal(bufs[X]).astype(np.float32),
+              S: rng.standard_normal(bufs[S]).astype(np.float32),
+              R: rng.standard_normal(bufs[R]).astype(np.float32),
+              R2: rng.standard_normal(bufs[R2]).astype(np.float32)}
+    gpu = H.Gpu(cp)
+    for b, v in inputs.items():
+        gpu.write_buf(b, v)
+    gpu.run_ops(0, len(ops))
+    steps = gpu.steps()
+    kernels = gpu.launches()
+    got = gpu.read_buf(OUT).reshape(bufs[OUT])
+    print("steps", steps)
+    print("launches", kernels)
+    assert steps[0][2].startswith("mx_chan_scale_add_stats_c%d" % c), steps
+    assert not any(kn.startswith("mx_chan_ln") for _, kn in kernels), kernels
+    # a run starting after the producer: the statistics pass runs itself
+    z_full = gpu.read_buf(Z)
+    a_full = gpu.read_buf(A)
+    gpu.poison()
+    gpu.write_buf(Z, z_full)
+    gpu.write_buf(A, a_full)
+    gpu.run_ops(4, len(ops))
+    part = gpu.read_buf(OUT).reshape(bufs[OUT])
+    gpu.set_fusion(False)
+    for b, v in inputs.items():
+        gpu.write_buf(b, v)
+    gpu.run_ops(0, len(ops))
+    plain = gpu.read_buf(OUT).reshape(bufs[OUT])
+    gpu.close()
+    assert np.array_equal(got.view(np.uint32), plain.view(np.uint32)), "fused and unfused passes differ"
+    assert np.array_equal(part.view(np.uint32), plain.view(np.uint32)), "the partial run differs"
+    want = oracle_plan(cp, inputs, OUT)
+    err = float(np.abs(got.astype(np.float64) - want).max())
+    print("max-abs vs CPU %.3g (max|cpu| %.3g)" % (err, float(np.abs(want).max())))
+    assert err <= 1e-3, err
