@@ -41,7 +41,7 @@ struct Launch {
     unsigned g[3] = {1, 1, 1};
     unsigned b[3] = {MXK_BLOCK, 1, 1};
     unsigned shm = 0;  // dynamic LDS bytes
-    alignas(16) unsigned char a0[320];
+    alignas(16) unsigned char a0[384];
     alignas(16) unsigned char a1[32];
     int nparams = 1;
     int kind = 0;  // 1: a0 holds GemmArgs (plain epilogue), 2: ConvArgs
@@ -138,6 +138,35 @@ struct ResizeTab {
     const float *t;
     int32_t maxt, pad;
 };
+
+// The multiplier and shift that divide every n < 2^31 by d (1 <= d < 2^31)
+// as umulhi(2 n, m) >> s: with s = ceil(log2 d) and m = ceil(2^(31+s) / d),
+// m d - 2^(31+s) < d <= 2^s, so n (m d - 2^(31+s)) < 2^(31+s) and the
+// quotient's floor is exact; m < 2^32 since d > 2^(s-1).
+void div_magic(uint32_t d, uint32_t &m, int32_t &s) {
+    int l = 0;
+    while ((1ULL << l) < d) ++l;
+    m = (uint32_t)(((1ULL << (31 + l)) + d - 1) / d);
+    s = l;
+}
+
+// The block map of BlockPerm q (cells fh x fw in a gh x gw grid of a wd-wide
+// plane), with its divisions as multiplies.
+BlockMap mx_block_map(const mx_op &q, int32_t r1map) {
+    BlockMap b{};
+    b.plane = q.h * q.wd;
+    b.on = 1;
+    b.fh = (int32_t)q.p[2];
+    b.fw = (int32_t)q.p[3];
+    b.gw = (int32_t)q.p[1];
+    b.wd = (int32_t)q.wd;
+    b.r1map = r1map;
+    div_magic((uint32_t)b.plane, b.mpl, b.spl);
+    div_magic((uint32_t)(b.fh * b.fw), b.mpp, b.spp);
+    div_magic((uint32_t)b.gw, b.mgw, b.sgw);
+    div_magic((uint32_t)b.fw, b.mfw, b.sfw);
+    return b;
+}
 
 // The LayerNorm tile kernel for c in {32, 64, 128}: c x P pixels per block,
 // the widest P (up to 8192 / c) that still gives four blocks per CU (two at
@@ -1954,8 +1983,7 @@ void Gpu::build_program(const mx_plan_desc *p) {
         if (!strncmp(l.name, "mx_pw_", 6) && aligned(dev(sp.out), 16)) {
             GemmArgs a;
             memcpy(&a, l.a0, sizeof a);
-            a.ymap = BlockMap{q.h * q.wd, 1, (int32_t)q.p[2], (int32_t)q.p[3], (int32_t)q.p[1], (int32_t)q.wd,
-                              sp.rperm >= 0 ? 1 : 0};
+            a.ymap = mx_block_map(q, sp.rperm >= 0 ? 1 : 0);
             set_args(l, a);
             return {l};
         }
@@ -1986,7 +2014,7 @@ void Gpu::build_program(const mx_plan_desc *p) {
         GemmArgs a;
         memcpy(&a, l.a0, sizeof a);
         a.B = dev(sp.xsrc);
-        a.xmap = BlockMap{q.h * q.wd, 1, (int32_t)q.p[2], (int32_t)q.p[3], (int32_t)q.p[1], (int32_t)q.wd, 0};
+        a.xmap = mx_block_map(q, 0);
         set_args(l, a);
     };
     // A GEMM step that also computes the LayerNorm of an output band (lno):
@@ -2230,7 +2258,7 @@ void Gpu::build_program(const mx_plan_desc *p) {
         a.ln = LnIn{stats, stats + ln.hw, la.scale, la.bias};
         if (xmap) {
             const mx_op &q = p->ops[sp.xperm];
-            a.xmap = BlockMap{q.h * q.wd, 1, (int32_t)q.p[2], (int32_t)q.p[3], (int32_t)q.p[1], (int32_t)q.wd, 0};
+            a.xmap = mx_block_map(q, 0);
         }
         set_args(gl, a);
         Step st{sp.first, sp.last, {}};

@@ -165,6 +165,11 @@ struct LnIn {
 struct BlockMap {
     int64_t plane;
     int32_t on, fh, fw, gw, wd, r1map;
+    // The map's divisions (by plane, fh * fw, gw and fw) as multiplies:
+    // n / d = umulhi(2 n, m) >> s for every n < 2^31, with s = ceil(log2 d)
+    // and m = ceil(2^(31 + s) / d), set by the host (mx_block_map).
+    uint32_t mpl, mpp, mgw, mfw;
+    int32_t spl, spp, sgw, sfw;
 };
 
 // A channel LayerNorm of a channel-major GEMM's output (the streaming

@@ -52,11 +52,13 @@ __device__ __forceinline__ float comp(const float4 &v, int t) {
 // so the loads of superstep s + 1 are in flight while superstep s multiplies.
 // The image index of blocked index e (0 <= e < plane) under map q (32-bit:
 // the host enables a map only below 2^31 elements).
+// n / d for n < 2^31, with the host's multiplier m and shift s for d.
+__device__ __forceinline__ uint32_t mdiv(uint32_t n, uint32_t m, int32_t s) { return __umulhi(n + n, m) >> s; }
 __device__ __forceinline__ uint32_t unblock(const BlockMap &q, uint32_t e) {
     const uint32_t pp = (uint32_t)(q.fh * q.fw);
-    const uint32_t gi = e / pp, p = e - gi * pp;
-    const uint32_t gy = gi / (uint32_t)q.gw, gx = gi - gy * (uint32_t)q.gw;
-    const uint32_t fy = p / (uint32_t)q.fw, fx = p - fy * (uint32_t)q.fw;
+    const uint32_t gi = mdiv(e, q.mpp, q.spp), p = e - gi * pp;
+    const uint32_t gy = mdiv(gi, q.mgw, q.sgw), gx = gi - gy * (uint32_t)q.gw;
+    const uint32_t fy = mdiv(p, q.mfw, q.sfw), fx = p - fy * (uint32_t)q.fw;
     return (gy * q.fh + fy) * q.wd + gx * q.fw + fx;
 }
 
@@ -109,11 +111,11 @@ __device__ void body(const GemmArgs &a) {
     // k's advance whole cell rows (CH: 16 % gw == 0) or whole pixel rows
     // (RW: 16 % fw == 0), and fw % 4 == 0 for the 128-bit reads.
     auto cell = [&](uint32_t r) -> int64_t {
-        const uint32_t gy = r / (uint32_t)xm.gw, gx = r - gy * (uint32_t)xm.gw;
+        const uint32_t gy = mdiv(r, xm.mgw, xm.sgw), gx = r - gy * (uint32_t)xm.gw;
         return (int64_t)gy * xm.fh * xm.wd + (int64_t)gx * xm.fw;
     };
     auto pixel = [&](uint32_t c) -> int64_t {
-        const uint32_t fy = c / (uint32_t)xm.fw, fx = c - fy * (uint32_t)xm.fw;
+        const uint32_t fy = mdiv(c, xm.mfw, xm.sfw), fx = c - fy * (uint32_t)xm.fw;
         return (int64_t)fy * xm.wd + fx;
     };
     // CH: this lane's four columns, s0 + 16 (i % 4) + 4 (i / 4) .. + 3
@@ -267,16 +269,20 @@ __device__ void body(const GemmArgs &a) {
     auto placed = [&](int64_t off) -> int64_t {
         if (!a.ymap.on) return off;
         const uint32_t e = (uint32_t)(cbase + off), pl = (uint32_t)a.ymap.plane;
-        const uint32_t base = e / pl * pl;
+        const uint32_t base = mdiv(e, a.ymap.mpl, a.ymap.spl) * pl;
         return (int64_t)(base + unblock(a.ymap, e - base)) - cbase;
     };
+    // Each slot's stored position is computed once, with its operands, and
+    // serves both the residual read at that position and the store.
     float4 ou[2], o1[2], o2[2];
+    int64_t pb[2] = {0, 0};
     auto operands = [&](int k, int buf) {
         int64_t off;
         const bool ok = where(k, off);
         const int64_t at = cbase + (ok ? off : 0);
+        pb[buf] = placed(ok ? off : 0);
         if (a.e.u) ou[buf] = ld4(a.e.u + at);
-        if (a.e.r1) o1[buf] = ld4(a.e.r1 + (a.ymap.r1map ? cbase + placed(ok ? off : 0) : at));
+        if (a.e.r1) o1[buf] = ld4(a.e.r1 + (a.ymap.r1map ? cbase + pb[buf] : at));
         if (a.e.r2) o2[buf] = ld4(a.e.r2 + at);
     };
     // LNO: the wave whose tile is the output LayerNorm's channels keeps its
@@ -378,7 +384,7 @@ __device__ void body(const GemmArgs &a) {
                 vs[k] = make_float4(v[0], v[1], v[2], v[3]);
             if (!a.lo.keep) continue;
         }
-        st4(Y + placed(off), make_float4(v[0], v[1], v[2], v[3]));
+        st4(Y + (FUSED ? pb[k & 1] : placed(off)), make_float4(v[0], v[1], v[2], v[3]));
     }
     if constexpr (LNO) {
         // Per pixel, the LayerNorm's statistics in the LayerNorm kernels'
