@@ -250,15 +250,18 @@ __device__ void body(const GemmArgs &a) {
     // Slot k of this lane: (mt, x) = (k / 4, k % 4) with KS = 1, and
     // (k, wave) with KS = 4 (the wave's share of the slots).
     constexpr int NK = KS == 1 ? 4 * TMW : TMW;
+    // (the lane's first slot offset once; the others differ from it by a
+    // wave-uniform amount)
+    const int64_t obase = LAYOUT == CH ? (int64_t)(w0 + i) * N + s0 + 4 * g : (int64_t)(s0 + i) * N + w0 + 4 * g;
     auto where = [&](int k, int64_t &off) -> bool {
         const int mt = KS == 1 ? k / 4 : k, x = KS == 1 ? k % 4 : wave;
         if (LAYOUT == CH) {
             const int m = w0 + mt * 16 + i, n = s0 + 16 * x + 4 * g;
-            off = (int64_t)m * N + n;
+            off = obase + (int64_t)(mt * 16) * N + 16 * x;
             return m < M && n < N;
         }
         const int row = s0 + 16 * x + i, c = w0 + mt * 16 + 4 * g;
-        off = (int64_t)row * N + c;
+        off = obase + (int64_t)(16 * x) * N + mt * 16;
         return row < M && c < N;
     };
     // The fused epilogue's operands are fetched one slot ahead, so their
@@ -302,9 +305,11 @@ __device__ void body(const GemmArgs &a) {
         if (LNO && KS == 4) vs[k] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
         if (FUSED && k + 1 < NK) operands(k + 1, (k + 1) & 1);
         const int mt = KS == 1 ? k / 4 : k, x = KS == 1 ? k % 4 : wave;
+        // Out-of-range slots run the arithmetic on clamped operands and skip
+        // only the global stores, so the uniform branches below stay
+        // uniform (no lane-divergent region around them).
         int64_t off;
         const bool inside = where(k, off);
-        if (!CT && !inside) continue;  // CT: both lanes of a pair share this, and both shuffle
         float v[4];
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
@@ -384,7 +389,7 @@ __device__ void body(const GemmArgs &a) {
                 vs[k] = make_float4(v[0], v[1], v[2], v[3]);
             if (!a.lo.keep) continue;
         }
-        st4(Y + (FUSED ? pb[k & 1] : placed(off)), make_float4(v[0], v[1], v[2], v[3]));
+        if (inside) st4(Y + (FUSED ? pb[k & 1] : placed(off)), make_float4(v[0], v[1], v[2], v[3]));
     }
     if constexpr (LNO) {
         // Per pixel, the LayerNorm's statistics in the LayerNorm kernels'
