@@ -158,6 +158,7 @@ __device__ __forceinline__ void ca_mlp_body(const CaArgs &a, const float *x) {
     for (int j = threadIdx.x; j < a.r; j += MXK_BLOCK) {
         const float *w = a.w1 + (int64_t)j * a.c;
         float acc = a.b1 ? a.b1[j] : 0.0f;
+#pragma unroll 16
         for (int i = 0; i < a.c; ++i) acc += w[i] * x[i];
         h[j] = acc >= 0.0f ? acc : a.slope * acc;
     }
@@ -165,6 +166,7 @@ __device__ __forceinline__ void ca_mlp_body(const CaArgs &a, const float *x) {
     for (int o = threadIdx.x; o < a.c; o += MXK_BLOCK) {
         const float *w = a.w2 + (int64_t)o * a.r;
         float acc = a.b2 ? a.b2[o] : 0.0f;
+#pragma unroll 16
         for (int j = 0; j < a.r; ++j) acc += w[j] * h[j];
         a.y[o] = 1.0f / (1.0f + expf(-acc));
     }

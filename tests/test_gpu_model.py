@@ -122,10 +122,11 @@ def test_timeline_and_counters(gpu_ok):
     assert np.allclose(sums, per, rtol=1e-5, atol=1e-6) and abs(ms.sum() - total) < 1e-3 * total + 1e-3
 
 
-@pytest.mark.parametrize("variant,side", [("S-2", 128), ("S-3", 64)])
+@pytest.mark.parametrize("variant,side", [("S-2", 128), ("S-3", 64), ("S-3", 448)])
 def test_fusion_is_bitwise_transparent(gpu_ok, variant, side):
     """The fused program applies each reader in its producer's epilogue with the
-    same float operations, so fused and unfused passes agree to the bit."""
+    same float operations, so fused and unfused passes agree to the bit (448:
+    planes large enough for many CALayer mean partials, tens per channel)."""
     from maxim_amd import plan as P
     from maxim_amd import hip as H
     plan = P.Plan(weights(variant), side, side)
