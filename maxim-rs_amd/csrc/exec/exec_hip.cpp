@@ -1739,7 +1739,7 @@ void Program::plan_fusion(const mx_plan_desc *p, bool require_clear) {
                 const mx_op &c = p->ops[S.first];
                 y = S.out;
                 hw = (uint64_t)c.hw;
-                if (ln.c != c.c) continue;
+                if (y < 0 || ln.c != c.c) continue;
             } else {
                 if (S.rule != RULE_NONE || S.lno >= 0 || S.xmul >= 0 || S.xperm >= 0) continue;
                 const uint64_t g = S.ln >= 0 ? S.first + 1 : S.first;
