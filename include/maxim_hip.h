@@ -138,6 +138,9 @@ uint64_t mxh_kernels_launched(mxh_gpu *g);
 const char *mxh_op_kernel(mxh_gpu *g, uint64_t i);
 /* Device facts for the roofline: compute units and peak engine clock (kHz). */
 int mxh_device_info(mxh_gpu *g, int *cus, int *clock_khz);
+/* Free and total device memory (bytes) of device 0, what Gpu::new sizes its
+ * refusal against (lightgpu `free_vram`, src/exec_gpu.rs:86-146). */
+int mxh_device_memory(uint64_t *free_bytes, uint64_t *total_bytes);
 
 #ifdef __cplusplus
 }

@@ -346,6 +346,8 @@ class Gpu {
 public:
     explicit Gpu(const mx_plan_desc *p);
     ~Gpu();
+    void init(const mx_plan_desc *p);
+    void release();
 
     HipApi &H;
     hipModule_t mod = nullptr;
@@ -665,7 +667,20 @@ void Gpu::validate(const mx_plan_desc *p) const {
     }
 }
 
+// A constructor that throws never runs the destructor, so every HIP object
+// created before a refusal or a later failure (module, stream, arena,
+// weights, scratch) is released here before the error propagates: a caller
+// that retries at a smaller size finds the device as it was.
 Gpu::Gpu(const mx_plan_desc *p) : H(hip()), doff(pg.doff) {
+    try {
+        init(p);
+    } catch (...) {
+        release();
+        throw;
+    }
+}
+
+void Gpu::init(const mx_plan_desc *p) {
     validate(p);
     check(H.hipInit(0), "hipInit");
     int ndev = 0;
@@ -677,6 +692,9 @@ Gpu::Gpu(const mx_plan_desc *p) : H(hip()), doff(pg.doff) {
     H.hipDeviceGetAttribute(&cus, kAttrMultiprocessorCount, 0);
     H.hipDeviceGetAttribute(&clock_khz, kAttrClockRate, 0);
     check(H.hipModuleLoadData(&mod, mx_kernels_hsaco), "hipModuleLoadData (embedded gfx950 code object)");
+    // The runtime reports an empty marketing name for devices its name table
+    // does not list; the code object only loads on gfx950, so that names it.
+    if (name.empty()) name = "AMD gfx950 (" + std::to_string(cus) + " CUs)";
     check(H.hipStreamCreate(&stream), "hipStreamCreate");
 
     // Device weights, in the layout each kernel reads, packed into one blob.
@@ -2291,7 +2309,9 @@ void Gpu::build_program(const mx_plan_desc *p) {
     }
 }
 
-Gpu::~Gpu() {
+Gpu::~Gpu() { release(); }
+
+void Gpu::release() {
     if (stream) H.hipStreamSynchronize(stream);
     if (gexec) H.hipGraphExecDestroy(gexec);
     if (graph) H.hipGraphDestroy(graph);
@@ -2300,6 +2320,13 @@ Gpu::~Gpu() {
     if (scratch) H.hipFree(scratch);
     if (stream) H.hipStreamDestroy(stream);
     if (mod) H.hipModuleUnload(mod);
+    gexec = nullptr;
+    graph = nullptr;
+    arena = nullptr;
+    wdev = nullptr;
+    scratch = nullptr;
+    stream = nullptr;
+    mod = nullptr;
 }
 
 }  // namespace mxh
@@ -2598,6 +2625,18 @@ int mxh_device_info(mxh_gpu *g, int *cus, int *clock_khz) {
     if (cus) *cus = G(g)->cus;
     if (clock_khz) *clock_khz = G(g)->clock_khz;
     return 0;
+}
+
+int mxh_device_memory(uint64_t *free_bytes, uint64_t *total_bytes) {
+    return guard([&] {
+        auto &H = mxh::hip();
+        mxh::check(H.hipInit(0), "hipInit");
+        mxh::check(H.hipSetDevice(0), "hipSetDevice");
+        size_t f = 0, t = 0;
+        mxh::check(H.hipMemGetInfo(&f, &t), "hipMemGetInfo");
+        if (free_bytes) *free_bytes = f;
+        if (total_bytes) *total_bytes = t;
+    });
 }
 
 }  // extern "C"

@@ -61,6 +61,7 @@ def _lib():
             "mxh_kernels_launched": (U, [V]),
             "mxh_op_kernel": (C.c_char_p, [V, U]),
             "mxh_device_info": (I, [V, C.POINTER(C.c_int), C.POINTER(C.c_int)]),
+            "mxh_device_memory": (I, [C.POINTER(C.c_uint64), C.POINTER(C.c_uint64)]),
         }
         for name, (res, args) in sig.items():
             f = getattr(L, name)
@@ -73,6 +74,13 @@ def _lib():
 def _check(rc):
     if rc != 0:
         raise P.MaximError(P.last_error())
+
+
+def device_memory():
+    """(free, total) bytes of device 0."""
+    f, t = C.c_uint64(), C.c_uint64()
+    _check(_lib().mxh_device_memory(C.byref(f), C.byref(t)))
+    return f.value, t.value
 
 
 def driver_ready():
