@@ -48,6 +48,21 @@ int mxh_run(mxh_gpu *g, const mx_plan_desc *plan, const float *input, uint64_t n
 int mxh_begin(mxh_gpu *g, const mx_plan_desc *plan, const float *input, uint64_t n_in);
 /* Gpu::step_op (src/exec_gpu.rs:348-352): execute exactly op `i`. */
 int mxh_step_op(mxh_gpu *g, const mx_plan_desc *plan, uint64_t i);
+/* No counterpart in the reference: for callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc). mxh_run's pass with device-resident input and output
+ * (d_input, d_output: device pointers of n_in / n_out floats) that allocates
+ * nothing: the executor's arena and weights (allocated once by mxh_new) hold
+ * the pass, and the kernels' scratch (channel-mean partial sums, LayerNorm
+ * statistics) is the code object's static array of 32 MiB per device, in
+ * place of the per-executor scratch mxh_run uses. A plan whose scratch needs
+ * more (e.g. 4096x4096) is refused with the numbers. Asynchronous on the
+ * executor's stream (mxh_sync waits). Every call on a device shares that
+ * device's array: calls that overlap on one device (executors run on their
+ * own streams) race, so let one finish before another starts. Every pass
+ * writes the scratch before reading it, so nothing needs clearing. */
+int mxh_run_noalloc(mxh_gpu *g, const mx_plan_desc *plan, const float *d_input, uint64_t n_in, float *d_output,
+                    uint64_t n_out);
 /* Every op over the image already in the arena as ONE captured HIP graph
  * (captured on the first call, replayed after), asynchronously. The graph
  * launches exactly the kernels mxh_run_ops would, in the same order. */

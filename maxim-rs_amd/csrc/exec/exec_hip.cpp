@@ -17,6 +17,7 @@
 #include <functional>
 #include <map>
 #include <memory>
+#include <mutex>
 #include <set>
 #include <string>
 #include <vector>
@@ -34,6 +35,49 @@ namespace mxh {
 using mx::Error;
 
 namespace {
+
+// The embedded code object, loaded once per device and kept until the
+// process ends (every executor on the device launches from it), with the
+// device address of its `scratch` array, the scratch of mxh_run_noalloc.
+// The code object is loaded through the module API, so the array is found
+// by name in the loaded module (hipModuleGetGlobal): the device address,
+// looked up with the device current, never the host-side name.
+struct DeviceCode {
+    hipModule_t mod = nullptr;
+    float *scratch = nullptr;
+    size_t scratch_bytes = 0;
+};
+
+constexpr int kMaxDevices = 64;
+
+DeviceCode &device_code(HipApi &H, int dev) {
+    static std::mutex mu;
+    static DeviceCode codes[kMaxDevices];
+    if (dev < 0 || dev >= kMaxDevices) throw Error("device ordinal out of range");
+    std::lock_guard<std::mutex> lock(mu);
+    DeviceCode &dc = codes[dev];
+    if (!dc.mod) {
+        check(H.hipSetDevice(dev), "hipSetDevice");
+        hipModule_t m = nullptr;
+        check(H.hipModuleLoadData(&m, mx_kernels_hsaco), "hipModuleLoadData (embedded gfx950 code object)");
+        void *p = nullptr;
+        size_t n = 0;
+        const hipError_t rc = H.hipModuleGetGlobal(&p, &n, m, "scratch");
+        if (rc != 0) {
+            H.hipModuleUnload(m);
+            check(rc, "hipModuleGetGlobal(scratch)");
+        }
+        if (!p || n < (size_t)MXK_NOALLOC_SCRATCH_FLOATS * 4) {
+            H.hipModuleUnload(m);
+            throw Error("the code object's scratch array is missing or smaller than " +
+                        std::to_string((size_t)MXK_NOALLOC_SCRATCH_FLOATS * 4) + " bytes");
+        }
+        dc.scratch = static_cast<float *>(p);
+        dc.scratch_bytes = n;
+        dc.mod = m;
+    }
+    return dc;
+}
 
 struct Launch {
     hipFunction_t f = nullptr;
@@ -429,6 +473,9 @@ public:
         }
     }
     std::vector<Step> prog;
+    // The fused program with every scratch pointer in the code object's
+    // static scratch (empty when this plan needs more than it holds).
+    std::vector<Step> prog_na;
     bool fusion = true;
     Program pg;                   // the fusion decisions and the device layout
     std::vector<uint64_t> &doff;  // = pg.doff
@@ -691,7 +738,8 @@ void Gpu::init(const mx_plan_desc *p) {
     if (H.hipDeviceGetName(nm, sizeof nm - 1, 0) == 0) name = nm;
     H.hipDeviceGetAttribute(&cus, kAttrMultiprocessorCount, 0);
     H.hipDeviceGetAttribute(&clock_khz, kAttrClockRate, 0);
-    check(H.hipModuleLoadData(&mod, mx_kernels_hsaco), "hipModuleLoadData (embedded gfx950 code object)");
+    const DeviceCode &dc = device_code(H, 0);
+    mod = dc.mod;
     // The runtime reports an empty marketing name for devices its name table
     // does not list; the code object only loads on gfx950, so that names it.
     if (name.empty()) name = "AMD gfx950 (" + std::to_string(cus) + " CUs)";
@@ -875,6 +923,23 @@ void Gpu::init(const mx_plan_desc *p) {
 
     build_launches(p, woff, extra, maxt);
     build_program(p);
+
+    // The same program over the code object's static scratch, for
+    // mxh_run_noalloc: the launches differ only in their scratch pointers.
+    if (scratch_len * 4 <= dc.scratch_bytes) {
+        float *own = scratch;
+        auto ops0 = std::move(ops);
+        auto alt0 = std::move(alt);
+        auto prog0 = std::move(prog);
+        scratch = dc.scratch;
+        build_launches(p, woff, extra, maxt);
+        build_program(p);
+        prog_na = std::move(prog);
+        ops = std::move(ops0);
+        alt = std::move(alt0);
+        prog = std::move(prog0);
+        scratch = own;
+    }
 }
 
 void Gpu::build_launches(const mx_plan_desc *p, const std::vector<int64_t> &woff,
@@ -2319,7 +2384,6 @@ void Gpu::release() {
     if (wdev) H.hipFree(wdev);
     if (scratch) H.hipFree(scratch);
     if (stream) H.hipStreamDestroy(stream);
-    if (mod) H.hipModuleUnload(mod);
     gexec = nullptr;
     graph = nullptr;
     arena = nullptr;
@@ -2422,6 +2486,31 @@ int mxh_run(mxh_gpu *g, const mx_plan_desc *plan, const float *input, uint64_t n
             else for (uint64_t i = 0; i < plan->n_ops; ++i) x.run_op(i);
         }
         x.read(x.doff[plan->output], output, n_out);
+    });
+}
+
+int mxh_run_noalloc(mxh_gpu *g, const mx_plan_desc *plan, const float *d_input, uint64_t n_in, float *d_output,
+                    uint64_t n_out) {
+    return guard([&] {
+        Gpu &x = *G(g);
+        x.check_plan(plan);
+        const mx_bufshape &si = plan->bufs[plan->input], &so = plan->bufs[plan->output];
+        if (n_in != (uint64_t)(si.c * si.h * si.w)) throw mx::Error("the input image and the plan's input buffer disagree");
+        if (n_out != (uint64_t)(so.c * so.h * so.w)) throw mx::Error("the output buffer and the plan's output disagree");
+        if (!d_input || !d_output) throw mx::Error("mxh_run_noalloc: no input or output");
+        if (x.prog_na.empty())
+            throw mx::Error("this pass needs " + std::to_string(x.scratch_len * 4) +
+                            " bytes of scratch; the static scratch of mxh_run_noalloc holds " +
+                            std::to_string((uint64_t)MXK_NOALLOC_SCRATCH_FLOATS * 4) + " (mxh_run has no such limit)");
+        auto &H = x.H;
+        mxh::check(H.hipMemcpyAsync(x.arena + x.doff[plan->input], d_input, n_in * 4, mxh::kMemcpyD2D, x.stream),
+                   "hipMemcpyAsync(input)");
+        for (mxh::Step &st : x.prog_na) {
+            for (auto &l : st.launches) x.launch(l);
+            x.launched += st.last - st.first;
+        }
+        mxh::check(H.hipMemcpyAsync(d_output, x.arena + x.doff[plan->output], n_out * 4, mxh::kMemcpyD2D, x.stream),
+                   "hipMemcpyAsync(output)");
     });
 }
 

@@ -8,6 +8,10 @@
 
 #define MXK_BLOCK 256
 
+// Floats in the code object's `scratch` array (32 MiB): the most scratch a
+// plan run through mxh_run_noalloc may need.
+#define MXK_NOALLOC_SCRATCH_FLOATS (8u << 20)
+
 // Flat elementwise ops over n elements.
 enum { MXK_COPY = 0, MXK_ADD, MXK_MUL, MXK_GATE_APPLY, MXK_GELU, MXK_LRELU, MXK_SIGMOID };
 

@@ -62,6 +62,7 @@ def _lib():
             "mxh_op_kernel": (C.c_char_p, [V, U]),
             "mxh_device_info": (I, [V, C.POINTER(C.c_int), C.POINTER(C.c_int)]),
             "mxh_device_memory": (I, [C.POINTER(C.c_uint64), C.POINTER(C.c_uint64)]),
+            "mxh_run_noalloc": (I, [V, D, V, U, V, U]),
         }
         for name, (res, args) in sig.items():
             f = getattr(L, name)
@@ -114,6 +115,13 @@ class Gpu:
         out = np.empty((c, h, w), np.float32)
         _check(_lib().mxh_run(self._h, self._d, img.ctypes.data, img.size, out.ctypes.data, out.size))
         return out
+
+    def run_noalloc(self, d_input, d_output):
+        """mxh_run_noalloc: the pass from device pointer d_input to d_output
+        (integers), asynchronously, with no allocation (the static scratch)."""
+        c, h, w = self.plan.bufs[self.plan.input]
+        co, ho, wo = self.plan.bufs[self.plan.output]
+        _check(_lib().mxh_run_noalloc(self._h, self._d, d_input, c * h * w, d_output, co * ho * wo))
 
     def begin(self, image):
         img = np.ascontiguousarray(image, dtype=np.float32)
