@@ -12,6 +12,7 @@
 #include <algorithm>
 #include <array>
 #include <cmath>
+#include <cstdio>
 #include <cstdlib>
 #include <cstring>
 #include <functional>
@@ -481,6 +482,7 @@ public:
     std::vector<uint64_t> &doff;  // = pg.doff
     uint64_t plan_arena_len = 0;
     void build_program(const mx_plan_desc *p);
+    void specialise(Launch &l);
     void sync() { check(H.hipStreamSynchronize(stream), "hipStreamSynchronize"); }
     // All ops with an event before each and one after the last; one sync.
     // Every step (one op, or one fused launch standing for several) with an
@@ -2372,6 +2374,42 @@ void Gpu::build_program(const mx_plan_desc *p) {
         so_apply(sp, st);
         prog.push_back(st);
     }
+    for (Step &st : prog) {
+        for (Launch &l : st.launches) specialise(l);
+        for (Launch &l : st.pre) specialise(l);
+    }
+}
+
+// A fused streaming kernel (mx_pw_..._f or _f_lo) specialised for the
+// epilogue operand set its launch uses (..._e<mask>, the pw::EP_* bits),
+// where the code object has one: the same arithmetic in the same order,
+// without the per-slot tests of the argument block.
+void Gpu::specialise(Launch &l) {
+    if (l.kind != 1 || strncmp(l.name, "mx_pw_", 6)) return;
+    const std::string nm = l.name;
+    auto ends = [&](const char *t) {
+        const size_t n = strlen(t);
+        return nm.size() > n && nm.compare(nm.size() - n, n, t) == 0;
+    };
+    if (!ends("_f") && !ends("_f_lo")) return;
+    GemmArgs a;
+    memcpy(&a, l.a0, sizeof a);
+    const int ep = (a.e.u ? 1 : 0) | (a.e.r1 ? 2 : 0) | (a.e.r2 ? 4 : 0) | (a.e.act == MXK_ACT_GELU ? 8 : 0) |
+                   (a.e.act == MXK_ACT_LRELU ? 16 : 0) | (a.ymap.on ? 32 : 0) | (a.bias ? 64 : 0) |
+                   (a.ymap.on && a.ymap.r1map ? 128 : 0);
+    const std::string sn = nm + "_e" + std::to_string(ep);
+    auto it = fns_.find(sn);
+    hipFunction_t f = nullptr;
+    if (it != fns_.end()) {
+        f = it->second;
+    } else {
+        if (H.hipModuleGetFunction(&f, mod, sn.c_str()) != 0) f = nullptr;
+        fns_[sn] = f;
+        if (!f && std::getenv("MAXIM_EP_LOG")) fprintf(stderr, "maxim: no specialised %s\n", sn.c_str());
+    }
+    if (!f) return;
+    l.name = intern(sn);
+    l.f = f;
 }
 
 Gpu::~Gpu() { release(); }

@@ -62,9 +62,26 @@ __device__ __forceinline__ uint32_t unblock(const BlockMap &q, uint32_t e) {
     return (gy * q.fh + fy) * q.wd + gx * q.fw + fx;
 }
 
-template <int LAYOUT, int TMW, int KS, bool FUSED, bool LN, bool XM = false, bool XMUL = false, bool CT = false,
-          bool LNO = false>
+// The epilogue's operand set as a compile-time mask (EP >= 0), so that a
+// kernel specialised for it has no per-slot tests of the argument block and
+// its memory waits count exactly the loads each use needs; EP = -1 reads the
+// set from the argument block at run time (every combination, one kernel).
+enum { EP_U = 1, EP_R1 = 2, EP_R2 = 4, EP_GELU = 8, EP_LRELU = 16, EP_YMAP = 32, EP_BIAS = 64, EP_R1MAP = 128 };
+
+// LN: 0 no folded LayerNorm; 1 the LayerNorm's full expression on X
+// ((x - m) r w + c, w and c per input channel); 2 its scale and bias
+// already folded into the weights and bias by the host ((x - m) r only).
+template <int LAYOUT, int TMW, int KS, bool FUSED, int LN, bool XM = false, bool XMUL = false, bool CT = false,
+          bool LNO = false, int EP = -1>
 __device__ void body(const GemmArgs &a) {
+    const bool has_u = EP < 0 ? a.e.u != nullptr : (EP & EP_U) != 0;
+    const bool has_r1 = EP < 0 ? a.e.r1 != nullptr : (EP & EP_R1) != 0;
+    const bool has_r2 = EP < 0 ? a.e.r2 != nullptr : (EP & EP_R2) != 0;
+    const bool has_gelu = EP < 0 ? a.e.act == MXK_ACT_GELU : (EP & EP_GELU) != 0;
+    const bool has_lrelu = EP < 0 ? a.e.act == MXK_ACT_LRELU : (EP & EP_LRELU) != 0;
+    const bool has_ymap = EP < 0 ? a.ymap.on != 0 : (EP & EP_YMAP) != 0;
+    const bool has_bias = EP < 0 ? a.bias != nullptr : (EP & EP_BIAS) != 0;
+    const bool r1map = EP < 0 ? a.ymap.r1map != 0 : (EP & EP_R1MAP) != 0;
     constexpr int TW = 16 * TMW;    // weight outputs per tile
     constexpr int NACC = 16 * TMW;  // accumulator floats per lane
     const int lane = threadIdx.x & 63;
@@ -150,8 +167,10 @@ __device__ void body(const GemmArgs &a) {
     if (LN) {  // a single 1x1 conv (no batch): statistics indexed like X's columns
         lmean = ld4(a.ln.mean + xcol);
         lrstd = ld4(a.ln.rstd + xcol);
-        lsc = a.ln.scale + 4 * g + S0 * 16;
-        lbi = a.ln.bias + 4 * g + S0 * 16;
+        if (LN == 1) {
+            lsc = a.ln.scale + 4 * g + S0 * 16;
+            lbi = a.ln.bias + 4 * g + S0 * 16;
+        }
     }
     // A folded Mul: X = B * B2 elementwise, B2 read at X's offsets.
     const float *xq[4];
@@ -166,12 +185,22 @@ __device__ void body(const GemmArgs &a) {
         }
 #pragma unroll
         for (int mt = 0; mt < TMW; ++mt) wv[mt] = ld4(wp[mt] + s * 16);
-        if (LN) {
+        if (LN == 1) {
             lv[0] = ld4(lsc + s * 16);
             lv[1] = ld4(lbi + s * 16);
         }
     };
     auto norm = [&](float4 *xv, const float4 *lv) {
+        if (LN == 2) {
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                xv[q].x = (xv[q].x - lmean.x) * lrstd.x;
+                xv[q].y = (xv[q].y - lmean.y) * lrstd.y;
+                xv[q].z = (xv[q].z - lmean.z) * lrstd.z;
+                xv[q].w = (xv[q].w - lmean.w) * lrstd.w;
+            }
+            return;
+        }
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
             const float w = comp(lv[0], q), c = comp(lv[1], q);
@@ -212,7 +241,7 @@ __device__ void body(const GemmArgs &a) {
     float4 bias[TMW];
 #pragma unroll
     for (int mt = 0; mt < TMW; ++mt) {
-        if (!a.bias) continue;
+        if (!has_bias) continue;
         if (LAYOUT == CH) {
             const int m = min(w0 + mt * 16 + i, wout - 1);
             bias[mt].x = a.bias[CT ? (m % (2 * a.co)) >> 1 : m];  // CT: row (ky, oc, kx) has oc's bias
@@ -270,7 +299,7 @@ __device__ void body(const GemmArgs &a) {
     // Where output element off (counted from this batch's Y) is stored: off
     // itself, or its image position under a folded backward permutation.
     auto placed = [&](int64_t off) -> int64_t {
-        if (!a.ymap.on) return off;
+        if (!has_ymap) return off;
         const uint32_t e = (uint32_t)(cbase + off), pl = (uint32_t)a.ymap.plane;
         const uint32_t base = mdiv(e, a.ymap.mpl, a.ymap.spl) * pl;
         return (int64_t)(base + unblock(a.ymap, e - base)) - cbase;
@@ -284,9 +313,9 @@ __device__ void body(const GemmArgs &a) {
         const bool ok = where(k, off);
         const int64_t at = cbase + (ok ? off : 0);
         pb[buf] = placed(ok ? off : 0);
-        if (a.e.u) ou[buf] = ld4(a.e.u + at);
-        if (a.e.r1) o1[buf] = ld4(a.e.r1 + (a.ymap.r1map ? cbase + pb[buf] : at));
-        if (a.e.r2) o2[buf] = ld4(a.e.r2 + at);
+        if (has_u) ou[buf] = ld4(a.e.u + at);
+        if (has_r1) o1[buf] = ld4(a.e.r1 + (r1map ? cbase + pb[buf] : at));
+        if (has_r2) o2[buf] = ld4(a.e.r2 + at);
     };
     // LNO: the wave whose tile is the output LayerNorm's channels keeps its
     // final values for it (and stores them raw only when asked to): with
@@ -325,7 +354,7 @@ __device__ void body(const GemmArgs &a) {
                 v[u] = t + red[(3 * NACC + q) * 64 + lane];
             }
         }
-        if (a.bias) {
+        if (has_bias) {
             if (LAYOUT == CH) {
                 const float bb = bias[mt].x;
 #pragma unroll
@@ -340,26 +369,26 @@ __device__ void body(const GemmArgs &a) {
         }
         if (FUSED) {
             const int bi = k & 1;
-            if (a.e.u) {
+            if (has_u) {
                 v[0] = ou[bi].x * (v[0] + 1.0f);
                 v[1] = ou[bi].y * (v[1] + 1.0f);
                 v[2] = ou[bi].z * (v[2] + 1.0f);
                 v[3] = ou[bi].w * (v[3] + 1.0f);
             }
-            if (a.e.act == MXK_ACT_GELU) {
+            if (has_gelu) {
 #pragma unroll
                 for (int u = 0; u < 4; ++u) v[u] = gelu(v[u]);
-            } else if (a.e.act == MXK_ACT_LRELU) {
+            } else if (has_lrelu) {
 #pragma unroll
                 for (int u = 0; u < 4; ++u) v[u] = v[u] >= 0.0f ? v[u] : a.e.slope * v[u];
             }
-            if (a.e.r1) {
+            if (has_r1) {
                 v[0] = v[0] + o1[bi].x;
                 v[1] = v[1] + o1[bi].y;
                 v[2] = v[2] + o1[bi].z;
                 v[3] = v[3] + o1[bi].w;
             }
-            if (a.e.r2) {
+            if (has_r2) {
                 v[0] = v[0] + o2[bi].x;
                 v[1] = v[1] + o2[bi].y;
                 v[2] = v[2] + o2[bi].z;
@@ -513,7 +542,7 @@ __device__ void body(const GemmArgs &a) {
 #define MXK_PW(LNAME, LAYOUT, TMW)                                                                 \
     MXK_PW1(LNAME, LAYOUT, TMW, 1, false, false, ) MXK_PW1(LNAME, LAYOUT, TMW, 4, false, false, _k4) \
     MXK_PW1(LNAME, LAYOUT, TMW, 1, false, true, _xm) MXK_PW1(LNAME, LAYOUT, TMW, 4, false, true, _k4_xm)
-#define MXK_PW_LN(TMW) MXK_PW1(ch, CH, TMW, 1, true, false, _ln) MXK_PW1(ch, CH, TMW, 4, true, false, _k4_ln)
+#define MXK_PW_LN(TMW) MXK_PW1(ch, CH, TMW, 1, 1, false, _ln) MXK_PW1(ch, CH, TMW, 4, 1, false, _k4_ln)
 #define MXK_PW_CT(TMW, KS, SUF)                                                                    \
     extern "C" __global__ __launch_bounds__(256) void mx_pw_ch##TMW##SUF##_t(GemmArgs a) {          \
         pw::body<pw::CH, TMW, KS, false, false, false, false, true>(a);                             \
@@ -544,11 +573,45 @@ MXK_PW_CT(2, 1, )
 MXK_PW_CT(2, 4, _k4)
 MXK_PW_CT(4, 1, )
 MXK_PW_CT(4, 4, _k4)
-MXK_PW_LO(2, 1, false, )
-MXK_PW_LO(2, 4, false, _k4)
-MXK_PW_LO(2, 1, true, _ln)
-MXK_PW_LO(2, 4, true, _k4_ln)
-MXK_PW_LO(4, 1, false, )
-MXK_PW_LO(4, 4, false, _k4)
-MXK_PW_LO(4, 1, true, _ln)
-MXK_PW_LO(4, 4, true, _k4_ln)
+MXK_PW_LO(2, 1, 0, )
+MXK_PW_LO(2, 4, 0, _k4)
+MXK_PW_LO(2, 1, 1, _ln)
+MXK_PW_LO(2, 4, 1, _k4_ln)
+MXK_PW_LO(4, 1, 0, )
+MXK_PW_LO(4, 4, 0, _k4)
+MXK_PW_LO(4, 1, 1, _ln)
+MXK_PW_LO(4, 4, 1, _k4_ln)
+
+// mx_pw_..._f[_lo]_e<EP>: a fused streaming kernel specialised for one
+// epilogue operand set (pw::EP_* mask), for the combinations the MAXIM
+// program launches most; the host takes one when it exists and the generic
+// _f kernel otherwise (the same arithmetic in the same order).
+#define MXK_PW_E(NAME, LAYOUT, TMW, KS, LN, XM, XMUL, LNO, EP)                                     \
+    extern "C" __global__ __launch_bounds__(256) void NAME##_e##EP(GemmArgs a) {                  \
+        pw::body<pw::LAYOUT, TMW, KS, true, LN, XM, XMUL, false, LNO, EP>(a);                      \
+    }
+MXK_PW_E(mx_pw_ch2_ln_f_lo, CH, 2, 1, 1, false, false, true, 72)
+MXK_PW_E(mx_pw_ch4_k4_ln_f_lo, CH, 4, 4, 1, false, false, true, 72)
+MXK_PW_E(mx_pw_ch2_ln_f, CH, 2, 1, 1, false, false, false, 72)
+MXK_PW_E(mx_pw_ch2_k4_ln_f, CH, 2, 4, 1, false, false, false, 72)
+MXK_PW_E(mx_pw_ch2_f_lo, CH, 2, 1, 0, false, false, true, 64)
+MXK_PW_E(mx_pw_ch2_f_lo, CH, 2, 1, 0, false, false, true, 66)
+MXK_PW_E(mx_pw_ch2_k4_f_lo, CH, 2, 4, 0, false, false, true, 64)
+MXK_PW_E(mx_pw_ch2_k4_f_lo, CH, 2, 4, 0, false, false, true, 66)
+MXK_PW_E(mx_pw_ch4_k4_f_lo, CH, 4, 4, 0, false, false, true, 64)
+MXK_PW_E(mx_pw_ch4_k4_f_lo, CH, 4, 4, 0, false, false, true, 66)
+MXK_PW_E(mx_pw_ch1_f, CH, 1, 1, 0, false, false, false, 226)
+MXK_PW_E(mx_pw_ch2_f, CH, 2, 1, 0, false, false, false, 64)
+MXK_PW_E(mx_pw_ch2_f, CH, 2, 1, 0, false, false, false, 226)
+MXK_PW_E(mx_pw_ch2_k4_f, CH, 2, 4, 0, false, false, false, 64)
+MXK_PW_E(mx_pw_ch2_k4_f, CH, 2, 4, 0, false, false, false, 65)
+MXK_PW_E(mx_pw_ch2_k4_f, CH, 2, 4, 0, false, false, false, 66)
+MXK_PW_E(mx_pw_ch2_k4_f, CH, 2, 4, 0, false, false, false, 226)
+MXK_PW_E(mx_pw_ch1_mul_f, CH, 1, 1, 0, false, true, false, 66)
+MXK_PW_E(mx_pw_ch1_mul_f, CH, 1, 1, 0, false, true, false, 70)
+MXK_PW_E(mx_pw_ch2_mul_f, CH, 2, 1, 0, false, true, false, 66)
+MXK_PW_E(mx_pw_ch2_mul_f, CH, 2, 1, 0, false, true, false, 70)
+MXK_PW_E(mx_pw_ch2_k4_mul_f, CH, 2, 4, 0, false, true, false, 66)
+MXK_PW_E(mx_pw_ch2_k4_mul_f, CH, 2, 4, 0, false, true, false, 70)
+MXK_PW_E(mx_pw_rw2_k4_f, RW, 2, 4, 0, false, false, false, 65)
+MXK_PW_E(mx_pw_rw4_k4_f, RW, 4, 4, 0, false, false, false, 65)
