@@ -14,9 +14,18 @@ in HBM when the timed region starts. Prints ONE JSON line:
                 stream over K further (eager) passes; `traffic` = its measured
                 HBM-side bytes per launch (profiles/hbm_traffic_c4.md)
   cpu_baseline  the CPU path (oracle/, a C restatement of the reference's
-                src/exec_cpu.rs) timed on this host over one full pass
+                src/exec_cpu.rs) timed on this host: the median of three full
+                C4 passes on every host core the process may use, plus one
+                single-thread MAXIM-2S 256x256 (C1) pass for scaling
+  c5            the 4096x4096 configuration (C5, a 28.7 GiB arena): ms/image
+                over graph replays, the dominant kernel's rate there (its
+                tensors are far larger than the 256 MB Infinity Cache, so the
+                HBM figure is cache-free) and the whole pass's effective rate
+  validation    the last timed replay's output against the first (eager)
+                pass, bit for bit, and against the CPU path (max-abs, PSNR);
+                the run fails if they disagree
 
-  python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
+  python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-c5]
 """
 
 import argparse
@@ -68,7 +77,8 @@ def main():
     ap.add_argument("--eager", action="store_true",
                     help="time eager launches of the fused program instead of graph replays "
                          "(the same kernels; for tracing tools)")
-    ap.add_argument("--cpu-threads", type=int, default=min(16, os.cpu_count() or 1))
+    ap.add_argument("--no-c5", action="store_true", help="skip the 4096x4096 leg")
+    ap.add_argument("--cpu-threads", type=int, default=host_threads())
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build runs on one GPU only (a MAXIM pass is one image on one device; "
@@ -111,6 +121,11 @@ def main():
     gpu.sync()
     wall = time.perf_counter() - t_start
     ms_per_step = wall * 1e3 / args.steps
+    # The last timed pass's output: the replays must reproduce the first
+    # (eager) pass bit for bit (a program that dropped work, or an input
+    # overwritten between replays, would not).
+    out_last = gpu.read_buf(plan.output).reshape(out.shape)
+    same = bool(np.array_equal(out_last.view(np.uint32), out.view(np.uint32)))
 
     # Attribution: K more passes of the same program launched eagerly, each
     # launch timed by the start/stop events its dispatch records on the
@@ -169,9 +184,18 @@ def main():
               % (k, 100 * t / tot, n // args.steps, avg * 1e6, f / n / avg / 1e12, b / n / avg / 1e9),
               file=sys.stderr)
 
+    cus, clk = gpu.device_info()
+    device = {"name": gpu.device_name, "arch": "gfx950", "cus": cus, "clock_mhz": clk // 1000}
+    validation = {"replay_equals_first_pass": same}
     cpu = None
     if not args.no_cpu:
-        cpu = cpu_baseline(plan, pad.img, args.cpu_threads)
+        cpu, ref = cpu_baseline(plan, pad.img, args.cpu_threads)
+        err = float(np.abs(out_last.astype(np.float64) - ref).max())
+        mse = float(((np.clip(out_last, 0, 1) - np.clip(ref, 0, 1)).astype(np.float64) ** 2).mean())
+        validation["max_abs_vs_cpu"] = err
+        validation["psnr_db_vs_cpu"] = 10 * np.log10(1.0 / mse) if mse > 0 else float("inf")
+    gpu.close()
+    c5 = None if args.no_c5 else c5_leg(w, R)
 
     line = {
         "metric": METRIC,
@@ -192,8 +216,91 @@ def main():
                    "sum_of_op_bounds_ms": round(bound_s * 1e3, 2)},
         "roofline": roof,
         "cpu_baseline": cpu,
+        "device": device,
+        "c5": c5,
+        "validation": validation,
     }
     print(json.dumps(line), flush=True)
+    bad = not same or ("max_abs_vs_cpu" in validation and (validation["max_abs_vs_cpu"] > 2e-3 or
+                                                           validation["psnr_db_vs_cpu"] < 50.0))
+    if bad:
+        print("bench: the timed passes do not reproduce the reference output: %s" % validation, file=sys.stderr)
+        sys.exit(1)
+
+
+def host_threads():
+    """The host cores this process may use (OMP_NUM_THREADS when the host
+    sets it, as the GPU boxes do, else every core)."""
+    try:
+        return max(1, int(os.environ["OMP_NUM_THREADS"]))
+    except (KeyError, ValueError):
+        return os.cpu_count() or 1
+
+
+def cpu_model():
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def c5_leg(w, R, steps=3):
+    """C5: MAXIM-3S on a 4096x4096 image (uniform [0, 1) plus N(0, 0.05),
+    clipped), the same weights: ms/image over graph replays, the dominant
+    kernel's rate (its tensors are far larger than the Infinity Cache, so its
+    HBM figure is cache-free) and the whole pass's effective rate."""
+    from maxim_amd import plan as P
+    from maxim_amd import hip as H
+    rng = np.random.default_rng(5)
+    img = np.clip(rng.random((3, 4096, 4096)) + rng.normal(0, 0.05, (3, 4096, 4096)), 0, 1).astype(np.float32)
+    plan = P.Plan(w, 4096, 4096)
+    print("bench: C5 4096x4096, arena %.1f GiB" % (plan.arena_bytes / 2**30), file=sys.stderr, flush=True)
+    gpu = H.Gpu(plan)
+    try:
+        out = gpu.run(img)
+        assert np.isfinite(out).all(), "non-finite C5 output"
+        gpu.run_graph()
+        gpu.sync()
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            gpu.run_graph()
+        gpu.sync()
+        ms = (time.perf_counter() - t0) * 1e3 / steps
+        launches = gpu.launches()
+        cost = launch_costs(plan, gpu.steps(), launches, R)
+        _, tot = gpu.run_timed()
+        lt = gpu.launch_timeline()
+        per = collections.defaultdict(lambda: [0.0, 0, 0.0, 0.0])
+        for k, (st, kn) in enumerate(launches):
+            e = per[kn]
+            e[0] += float(lt[k])
+            e[1] += 1
+            e[2] += cost[k][0]
+            e[3] += cost[k][1]
+        kern, (tms, nl, fl, by) = max(per.items(), key=lambda kv: kv[1][0])
+        avg_s = tms / nl / 1e3
+        fl_all = sum(c[0] for c in cost)
+        by_all = sum(c[1] for c in cost)
+        if fl / by >= R.RIDGE:
+            dom = {"bound": "mfma", "achieved": fl / nl / avg_s / 1e12, "peak": 157.3, "unit": "TFLOP/s"}
+        else:
+            dom = {"bound": "hbm", "achieved": by / nl / avg_s / 1e9, "peak": 8000.0, "unit": "GB/s"}
+        dom["frac"] = dom["achieved"] / dom["peak"]
+        dom.update({"kernel": kern, "avg_launch_us": avg_s * 1e6, "launches_per_step": nl,
+                    "share_of_pass": tms / tot})
+        res = {"workload": "C5: MAXIM-3S, 4096x4096 RGB, one image per step", "ms_per_image": ms,
+               "images_per_s": 1e3 / ms, "steps": steps, "arena_gib": round(plan.arena_bytes / 2**30, 2),
+               "kernel_ms_per_pass": tot, "tflops_effective": fl_all / (ms * 1e-3) / 1e12,
+               "tb_per_s_effective": by_all / (ms * 1e-3) / 1e12,
+               "algorithmic_per_pass": {"gflop": fl_all / 1e9, "gb": by_all / 1e9}, "dominant": dom}
+        print("bench: C5 %.1f ms/image; dominant %s %.1f us x %d (%.1f%% of %s peak)"
+              % (ms, kern, avg_s * 1e6, nl, 100 * dom["frac"], dom["unit"]), file=sys.stderr, flush=True)
+        return res
+    finally:
+        gpu.close()
 
 
 TRAFFIC = os.path.join(ROOT, "profiles", "hbm_traffic_c4.md")
@@ -290,17 +397,42 @@ def launch_costs(plan, steps, launches, R):
 
 
 def cpu_baseline(plan, img, threads):
-    """The CPU path over one full pass of the same plan and image."""
+    """The CPU path (oracle/: a C restatement of src/exec_cpu.rs, OpenMP over
+    channels, rows and pixels) on this host: the median of three full C4
+    passes on `threads` cores, and one single-thread C1 pass (MAXIM-2S,
+    256x256) for scaling. Returns the record and the C4 output."""
     from oracle import oracle as O
-    arena = np.zeros(plan.arena_len, np.float32)
-    o = int(plan.offs[plan.input])
-    arena[o:o + img.size] = img.ravel()
-    t0 = time.perf_counter()
-    O.run(plan, arena, threads)
-    dt = time.perf_counter() - t0
-    return {"value": 1.0 / dt, "unit": "images/s", "cores": O.threads_used(), "kind": "port",
-            "sample": "one full MAXIM-3S 640x448 pass (2885 ops) of the C restatement of "
-                      "src/exec_cpu.rs, %.1f s" % dt}
+    from maxim_amd import plan as P
+
+    def one(pl, im, th):
+        arena = np.zeros(pl.arena_len, np.float32)
+        o = int(pl.offs[pl.input])
+        arena[o:o + im.size] = im.ravel()
+        t0 = time.perf_counter()
+        O.run(pl, arena, th)
+        dt = time.perf_counter() - t0
+        q = int(pl.offs[pl.output])
+        c, h, w = pl.bufs[pl.output]
+        return dt, arena[q:q + c * h * w].reshape(c, h, w).copy()
+
+    times, ref = [], None
+    for _ in range(3):
+        dt, ref = one(plan, img, threads)
+        times.append(dt)
+    used = O.threads_used()
+    med = float(np.median(times))
+    w2 = P.Weights.synthetic("S-2", seed=SEED, gain=GAIN, bias_std=0.02, ln_std=0.1)
+    c1 = P.Plan(w2, 256, 256)
+    dt1, _ = one(c1, np.random.default_rng(2).random((3, 256, 256), dtype=np.float32), 1)
+    print("bench: CPU C4 %s s on %d threads, C1 %.1f s on 1 thread (%s)"
+          % (", ".join("%.2f" % t for t in times), used, dt1, cpu_model()), file=sys.stderr, flush=True)
+    rec = {"value": 1.0 / med, "unit": "images/s", "cores": used, "kind": "port",
+           "sample": "median of 3 full MAXIM-3S 640x448 passes (2885 ops) of the C restatement of "
+                     "src/exec_cpu.rs: %s s" % ", ".join("%.2f" % t for t in times),
+           "cpu_model": cpu_model(), "host_cores_visible": os.cpu_count(),
+           "c1_single_thread": {"seconds": dt1, "images_per_s": 1.0 / dt1,
+                                "workload": "C1: MAXIM-2S 256x256, one pass, 1 thread"}}
+    return rec, ref
 
 
 if __name__ == "__main__":

@@ -128,3 +128,29 @@ def judge_op(plan, arena, op, got):
         ok = rel <= 1e-4
     key = "gemv" if exact and op.kind == P.CONV1X1 else name
     return ok, key, rel
+
+
+def rewrite_safetensors(path, new_value):
+    """Overwrite tensors of a safetensors file in place: new_value(name,
+    array) returns the replacement (same shape, float32) or None to keep the
+    tensor. The header is unchanged, so the file stays a valid checkpoint."""
+    import json
+    import struct
+    with open(path, "r+b") as f:
+        n = struct.unpack("<Q", f.read(8))[0]
+        header = json.loads(f.read(n))
+        base = 8 + n
+        for name, meta in header.items():
+            if name == "__metadata__":
+                continue
+            assert meta["dtype"] == "F32", meta
+            b, e = meta["data_offsets"]
+            f.seek(base + b)
+            old = np.frombuffer(f.read(e - b), np.float32).reshape(meta["shape"])
+            new = new_value(name, old)
+            if new is None:
+                continue
+            new = np.ascontiguousarray(new, np.float32)
+            assert new.shape == old.shape, (name, new.shape, old.shape)
+            f.seek(base + b)
+            f.write(new.tobytes())

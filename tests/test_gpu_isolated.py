@@ -93,6 +93,45 @@ def gmlp_range(plan):
     return x, y, first, last
 
 
+def test_c2_gmlp_layer_with_baseline_weights(gpu_ok, tmp_path):
+    """C2 as BASELINE.json names it: the split-head gMLP layer at c=32,
+    256x256, x ~ N(0, 1), with every Dense and LayerNorm parameter of the
+    layer ~ N(0, 0.02), written into a checkpoint file and read back through
+    the safetensors loader (the variant comes from the file)."""
+    from maxim_amd import plan as P
+    from maxim_amd import hip as H
+    from oracle import oracle as O
+    from conftest import rewrite_safetensors
+    path = str(tmp_path / "c2.safetensors")
+    weights("S-2").save(path)
+    prefix = "stage_0_encoder_block_0/SplitHeadMultiAxisGmlpLayer_0/"
+    g = np.random.default_rng(20)
+    touched = []
+
+    def n002(name, old):
+        if not name.startswith(prefix):
+            return None
+        touched.append(name)
+        return (0.02 * g.standard_normal(old.shape)).astype(np.float32)
+
+    rewrite_safetensors(path, n002)
+    assert len(touched) == 26, touched
+    w = P.Weights.open(path)
+    assert w.config.num_stages == 2 and w.config.features == 32
+    plan = P.Plan(w, 256, 256, named=True, deep=True)
+    x, y, first, last = gmlp_range(plan)
+    assert last - first == 25 and plan.bufs[x] == (32, 256, 256)
+    xin = np.random.default_rng(8).standard_normal(plan.buf_len(x)).astype(np.float32)
+    arena = np.zeros(plan.arena_len, np.float32)
+    arena[int(plan.offs[x]):int(plan.offs[x]) + xin.size] = xin
+    O.run_range(plan, arena, first, last)
+    gpu = H.Gpu(plan)
+    gpu.write_buf(x, xin)
+    gpu.run_ops(first, last)
+    got = gpu.read_buf(y)
+    check(got, buf(plan, arena, y), "C2 gMLP layer c=32 256x256, N(0, 0.02) parameters")
+
+
 def test_c2_gmlp_layer(gpu_ok):
     from maxim_amd import plan as P
     from maxim_amd import hip as H
@@ -109,3 +148,17 @@ def test_c2_gmlp_layer(gpu_ok):
     gpu.run_ops(first, last)
     got = gpu.read_buf(y)
     check(got, buf(plan, arena, y), "C2 gMLP layer c=32 256x256")
+
+
+def test_chan_ln_one_pass_variance_on_the_gpu(gpu_ok):
+    """The device LayerNorm keeps the reference's one-pass fp32 variance
+    (src/exec_cpu.rs:403-406): on pixels where a two-pass variance would
+    differ by orders of magnitude it gives the one-pass bits exactly."""
+    from maxim_amd import plan as P
+    from test_oracle import ln_one_pass_fp32, ln_variance_case
+    x, s, b = ln_variance_case()
+    c, h, w = x.shape
+    op = P.make_op(P.CHAN_LN, dst=1, src=0, scale=0, bias=1, c=c, hw=h * w)
+    got = run_one(op, [(c, h, w), (c, h, w)], [s, b], x)
+    want = ln_one_pass_fp32(x, s, b)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))

@@ -53,6 +53,13 @@ def test_c4_maxim_3s_600x400(gpu_ok):
     gpu, out = compare(plan, pad.img, "C4 S-3 640x448")
     crop = P.crop_out(out, pad)
     assert crop.shape == (3, 400, 600)
+    # The timed path (bench.py): replays of the captured graph are bitwise the
+    # eager fused pass just checked against the CPU path, replay after replay.
+    out = out.copy()
+    gpu.set_graph(True)
+    for rep in range(2):
+        got = gpu.run(pad.img)
+        assert np.array_equal(got.view(np.uint32), out.view(np.uint32)), rep
 
 
 def test_poison_and_determinism(gpu_ok):

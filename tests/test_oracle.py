@@ -98,6 +98,55 @@ def test_chan_ln_against_float64():
     assert np.abs(got[:, 0, 2] - want[:, 0, 2]).max() <= 0.05
 
 
+def ln_one_pass_fp32(x, s, b):
+    """The reference's LayerNorm in fp32, step by step (src/exec_cpu.rs:392-432):
+    ascending s1 = sum x and s2 = sum x^2, m = s1 / c, var = s2 / c - m^2,
+    r = 1 / sqrt(max(var, 0) + 1e-6), y = (x - m) * r * w + b."""
+    f = np.float32
+    c = x.shape[0]
+    s1 = np.zeros(x.shape[1:], f)
+    s2 = np.zeros(x.shape[1:], f)
+    for k in range(c):
+        s1 = (s1 + x[k]).astype(f)
+        s2 = (s2 + (x[k] * x[k]).astype(f)).astype(f)
+    m = (s1 / f(c)).astype(f)
+    var = (s2 / f(c) - (m * m).astype(f)).astype(f)
+    r = (f(1) / np.sqrt((np.maximum(var, f(0)) + f(1e-6)).astype(f))).astype(f)
+    return ((((x - m).astype(f) * r).astype(f) * s[:, None, None]).astype(f) + b[:, None, None]).astype(f)
+
+
+def ln_variance_case():
+    """Pixels where the one-pass fp32 variance and a two-pass one disagree by
+    orders of magnitude: a large common offset (1000, 5000) under a spread of
+    ~0.05, where s2 / c - m^2 cancels to a few ulps of m^2 (so r is far from
+    1 / 0.05), and a plain pixel for contrast."""
+    g = rng(31)
+    c = 32
+    x = np.empty((c, 1, 3), np.float32)
+    x[:, 0, 0] = np.float32(1000.0) + (0.05 * g.standard_normal(c)).astype(np.float32)
+    x[:, 0, 1] = np.float32(5000.0) + (0.05 * g.standard_normal(c)).astype(np.float32)
+    x[:, 0, 2] = g.standard_normal(c).astype(np.float32)
+    s = (1 + 0.1 * g.standard_normal(c)).astype(np.float32)
+    b = (0.1 * g.standard_normal(c)).astype(np.float32)
+    return x, s, b
+
+
+def test_chan_ln_one_pass_variance_known_answer():
+    """The variance is the reference's one-pass s2 / c - m^2 in fp32
+    (src/exec_cpu.rs:403-406), not a two-pass sum of squared deviations: on
+    pixels where the two differ by orders of magnitude the oracle gives the
+    one-pass bits exactly."""
+    x, s, b = ln_variance_case()
+    got = O().chan_ln(x, s, b)
+    want = ln_one_pass_fp32(x, s, b)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    # the case discriminates: a two-pass variance gives a different answer
+    xd = x.astype(np.float64)
+    two = (xd - xd.mean(0)) / np.sqrt(xd.var(0) + 1e-6) * s[:, None, None] + b[:, None, None]
+    assert np.abs(two[:, 0, :2] - want[:, 0, :2]).max() > 0.5
+    assert np.abs(two[:, 0, 2] - want[:, 0, 2]).max() < 1e-4
+
+
 def test_chan_mean():
     x = rng(9).standard_normal((6, 300, 11)).astype(np.float32) + 2
     assert rel_err(O().chan_mean(x), x.astype(np.float64).mean((1, 2))) <= 1e-6
