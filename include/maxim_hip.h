@@ -153,6 +153,13 @@ uint64_t mxh_kernels_launched(mxh_gpu *g);
 const char *mxh_op_kernel(mxh_gpu *g, uint64_t i);
 /* Device facts for the roofline: compute units and peak engine clock (kHz). */
 int mxh_device_info(mxh_gpu *g, int *cus, int *clock_khz);
+/* The enhancement run with the HIP backend, what a `--device hip` arm of the
+ * reference's CLI calls between reading and writing the PNG (src/main.rs
+ * 173-458): open the safetensors checkpoint (variant from the file), pad the
+ * [3][h][w] image (0..1) by the reference pipeline to a multiple of 64, build
+ * the release plan, run it on the device (refusing up front if it does not
+ * fit), and crop the prediction back to [3][h][w] in `out`. */
+int mxh_enhance(const char *checkpoint, const float *image, int64_t h, int64_t w, float *out);
 /* Free and total device memory (bytes) of device 0, what Gpu::new sizes its
  * refusal against (lightgpu `free_vram`, src/exec_gpu.rs:86-146). */
 int mxh_device_memory(uint64_t *free_bytes, uint64_t *total_bytes);

@@ -201,6 +201,14 @@ int mx_preprocess(const float *img, int64_t c, int64_t h, int64_t w, int64_t fac
 int mx_crop_out(const float *img, int64_t c, int64_t ph, int64_t pw, int64_t even_h,
                 int64_t even_w, int64_t orig_h, int64_t orig_w, float *out);
 
+/* image::read_png (src/image.rs:33-72): an 8-bit grayscale, gray + alpha, RGB
+ * or RGBA PNG as [3][h][w] floats in 0..1 (gray expanded, alpha dropped).
+ * Two calls: with out == NULL it reports h and w; then with 3*h*w floats. */
+int mx_png_read(const char *path, float *out, int64_t *h, int64_t *w);
+/* image::write_png (src/image.rs:74-104): [3][h][w] in 0..1 as an 8-bit RGB
+ * PNG, each value clamped and rounded half up. */
+int mx_png_write(const char *path, const float *img, int64_t h, int64_t w);
+
 /* memguard::CpuPlan::of / check (src/memguard.rs:61-172), for `threads` workers.
  * `avail_override` >= 0 replaces /proc/meminfo's MemAvailable (for tests).
  * Returns 0 when the CPU pass fits, -1 (with the reference's message) when not. */

@@ -2754,6 +2754,44 @@ int mxh_device_info(mxh_gpu *g, int *cus, int *clock_khz) {
     return 0;
 }
 
+int mxh_enhance(const char *checkpoint, const float *image, int64_t h, int64_t w, float *out) {
+    struct Owned {
+        mx_weights *w = nullptr;
+        mx_plan *p = nullptr;
+        mxh_gpu *g = nullptr;
+        ~Owned() {
+            if (g) mxh_free(g);
+            if (p) mx_plan_free(p);
+            if (w) mx_weights_free(w);
+        }
+    } o;
+    return guard([&] {
+        if (!image || !out) throw mx::Error("mxh_enhance: no image or output");
+        // The checkpoint says what it is (Weights::open derives the variant).
+        o.w = mx_weights_open(checkpoint);
+        if (!o.w) throw mx::Error(mx_last_error());
+        // The reference pipeline's padding: even-ize, then a centred reflect
+        // to a multiple of 64 (image::preprocess, src/image.rs:171-207).
+        int64_t ph = 0, pw = 0, eh = 0, ew = 0;
+        if (mx_preprocess(image, 3, h, w, 64, nullptr, &ph, &pw, &eh, &ew) != 0) throw mx::Error(mx_last_error());
+        std::vector<float> padded((size_t)(3 * ph * pw));
+        if (mx_preprocess(image, 3, h, w, 64, padded.data(), &ph, &pw, &eh, &ew) != 0)
+            throw mx::Error(mx_last_error());
+        // The release plan (no dump buffers), run on the device, cropped back
+        // centred on the even shape (image::crop_out, src/image.rs:232-246).
+        o.p = mx_plan_build(o.w, ph, pw, 0, 1, 0);
+        if (!o.p) throw mx::Error(mx_last_error());
+        mx_plan_desc d;
+        mx_plan_describe(o.p, &d);
+        o.g = mxh_new(&d);
+        if (!o.g) throw mx::Error(mx_last_error());
+        std::vector<float> pred((size_t)(3 * ph * pw));
+        if (mxh_run(o.g, &d, padded.data(), padded.size(), pred.data(), pred.size()) != 0)
+            throw mx::Error(mx_last_error());
+        if (mx_crop_out(pred.data(), 3, ph, pw, eh, ew, h, w, out) != 0) throw mx::Error(mx_last_error());
+    });
+}
+
 int mxh_device_memory(uint64_t *free_bytes, uint64_t *total_bytes) {
     return guard([&] {
         auto &H = mxh::hip();

@@ -615,3 +615,10 @@ MXK_PW_E(mx_pw_ch2_k4_mul_f, CH, 2, 4, 0, false, true, false, 66)
 MXK_PW_E(mx_pw_ch2_k4_mul_f, CH, 2, 4, 0, false, true, false, 70)
 MXK_PW_E(mx_pw_rw2_k4_f, RW, 2, 4, 0, false, false, false, 65)
 MXK_PW_E(mx_pw_rw4_k4_f, RW, 4, 4, 0, false, false, false, 65)
+MXK_PW_E(mx_pw_ch2_lnf_f_lo, CH, 2, 1, 2, false, false, true, 72)
+MXK_PW_E(mx_pw_ch2_lnf_f, CH, 2, 1, 2, false, false, false, 72)
+MXK_PW_E(mx_pw_ch2_k4_lnf_f, CH, 2, 4, 2, false, false, false, 72)
+MXK_PW_E(mx_pw_ch1_ln_f, CH, 1, 1, 1, false, false, false, 72)
+MXK_PW_E(mx_pw_ch1_lnf_f, CH, 1, 1, 2, false, false, false, 72)
+MXK_PW_E(mx_pw_ch4_ln_f_lo, CH, 4, 1, 1, false, false, true, 72)
+MXK_PW_E(mx_pw_ch4_ln_f, CH, 4, 1, 1, false, false, false, 72)

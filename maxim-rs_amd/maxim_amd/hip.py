@@ -63,6 +63,7 @@ def _lib():
             "mxh_device_info": (I, [V, C.POINTER(C.c_int), C.POINTER(C.c_int)]),
             "mxh_device_memory": (I, [C.POINTER(C.c_uint64), C.POINTER(C.c_uint64)]),
             "mxh_run_noalloc": (I, [V, D, V, U, V, U]),
+            "mxh_enhance": (I, [C.c_char_p, V, C.c_int64, C.c_int64, V]),
         }
         for name, (res, args) in sig.items():
             f = getattr(L, name)
@@ -82,6 +83,15 @@ def device_memory():
     f, t = C.c_uint64(), C.c_uint64()
     _check(_lib().mxh_device_memory(C.byref(f), C.byref(t)))
     return f.value, t.value
+
+
+def enhance(checkpoint, image):
+    """mxh_enhance: checkpoint file + [3][h][w] image -> the cropped
+    prediction (the reference's run with the HIP backend)."""
+    img = np.ascontiguousarray(image, np.float32)
+    out = np.empty_like(img)
+    _check(_lib().mxh_enhance(checkpoint.encode(), img.ctypes.data, img.shape[1], img.shape[2], out.ctypes.data))
+    return out
 
 
 def driver_ready():

@@ -114,6 +114,8 @@ def _declare(lib):
         "mx_crop_out": (C.c_int, [P, C.c_int64, C.c_int64, C.c_int64, C.c_int64, C.c_int64,
                                   C.c_int64, C.c_int64, P]),
         "mx_memguard_check": (C.c_int, [P, C.c_int, C.c_int64, C.POINTER(C.c_uint64)]),
+        "mx_png_read": (C.c_int, [C.c_char_p, P, C.POINTER(C.c_int64), C.POINTER(C.c_int64)]),
+        "mx_png_write": (C.c_int, [C.c_char_p, P, C.c_int64, C.c_int64]),
     }
     for name, (res, args) in sig.items():
         f = getattr(lib, name)
@@ -382,3 +384,19 @@ class CustomPlan:
 
     def weight(self, i):
         return self._weights[i]
+
+
+def read_png(path):
+    """image::read_png: an 8-bit PNG as a [3][h][w] float32 array in 0..1."""
+    h, w = C.c_int64(), C.c_int64()
+    _check(lib().mx_png_read(path.encode(), None, C.byref(h), C.byref(w)))
+    out = np.empty((3, h.value, w.value), np.float32)
+    _check(lib().mx_png_read(path.encode(), out.ctypes.data, C.byref(h), C.byref(w)))
+    return out
+
+
+def write_png(path, img):
+    """image::write_png: [3][h][w] in 0..1 as an 8-bit RGB PNG."""
+    a = np.ascontiguousarray(img, np.float32)
+    assert a.ndim == 3 and a.shape[0] == 3, a.shape
+    _check(lib().mx_png_write(path.encode(), a.ctypes.data, a.shape[1], a.shape[2]))

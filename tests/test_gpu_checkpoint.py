@@ -1,0 +1,66 @@
+"""The enhancement run end to end from files, on the device: a checkpoint
+written in the reference's safetensors layout and read back (the variant
+comes from the file, src/weights.rs:37-41, src/config.rs:71-100), a PNG
+input, the reference pipeline's padding, the HIP pass and the crop
+(src/main.rs:173-458) - through mxh_enhance and through the maxim_hip
+command - against the CPU path on the same file and pixels, at the
+north-star bar (max-abs 2e-3, PSNR >= 50 dB; the 8-bit outputs within one
+level)."""
+
+import os
+import subprocess
+
+import numpy as np
+import pytest
+
+from conftest import ROOT, psnr, run_oracle, smooth_image, weights
+
+pytestmark = pytest.mark.gpu
+
+
+def test_c4_from_checkpoint_and_png(gpu_ok, tmp_path):
+    from maxim_amd import plan as P
+    from maxim_amd import hip as H
+    ckpt = str(tmp_path / "maxim_s3.safetensors")
+    weights("S-3").save(ckpt)
+    src = str(tmp_path / "in.png")
+    P.write_png(src, smooth_image(400, 600, seed=4))
+    img = P.read_png(src)
+    assert img.shape == (3, 400, 600)
+    print("checkpoint: S-3 from file, 600x400 PNG", flush=True)
+    got = H.enhance(ckpt, img)
+
+    # the CPU path on the same file and pixels
+    w = P.Weights.open(ckpt)
+    assert w.config.num_stages == 3 and w.params == weights("S-3").params
+    pad = P.preprocess(img, 64)
+    plan = P.Plan(w, *pad.img.shape[1:])
+    arena = run_oracle(plan, pad.img)
+    o = int(plan.offs[plan.output])
+    pred = arena[o:o + pad.img.size].reshape(pad.img.shape)
+    ref = P.crop_out(pred, pad)
+    err = float(np.abs(got.astype(np.float64) - ref).max())
+    print("mxh_enhance vs CPU path: max-abs %.3g, PSNR %.1f dB" % (err, psnr(got, ref)), flush=True)
+    assert got.shape == (3, 400, 600) and err <= 2e-3 and psnr(got, ref) >= 50.0
+
+    # the command: PNG in, PNG out
+    out = str(tmp_path / "out.png")
+    exe = os.path.join(ROOT, "maxim-rs_amd", "lib", "maxim_hip")
+    r = subprocess.run([exe, "-m", ckpt, "-i", src, "-o", out], capture_output=True, text=True, timeout=300)
+    print(r.stderr, flush=True)
+    assert r.returncode == 0, r.stderr
+    cli = P.read_png(out)
+    want = str(tmp_path / "want.png")
+    P.write_png(want, ref)
+    levels = np.abs(np.rint(cli * 255) - np.rint(P.read_png(want) * 255))
+    print("maxim_hip vs CPU path: %d of %d samples one level apart" % (int((levels > 0).sum()), levels.size))
+    assert levels.max() <= 1.0
+
+
+def test_enhance_refuses_a_bad_checkpoint(gpu_ok, tmp_path):
+    from maxim_amd import plan as P
+    from maxim_amd import hip as H
+    bad = str(tmp_path / "bad.safetensors")
+    open(bad, "wb").write(b"\x08\x00\x00\x00\x00\x00\x00\x00{}      ")
+    with pytest.raises(P.MaximError):
+        H.enhance(bad, np.zeros((3, 64, 64), np.float32))

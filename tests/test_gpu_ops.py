@@ -19,34 +19,20 @@ BIT-EXACT:
 import numpy as np
 import pytest
 
-from conftest import EXACT, buf, judge_op, op_sources, smooth_image, weights
+from conftest import EXACT, judge_op, smooth_image, weights
 
 pytestmark = pytest.mark.gpu
 
 
 def walk(plan, img, report):
-    from maxim_amd import hip as H
+    """The package's lockstep walk with the stricter bars and the CPU path's
+    exact inputs before every op."""
+    from maxim_amd import devtools as D
     from oracle import oracle as O
-
-    arena = np.zeros(plan.arena_len, np.float32)
-    o = int(plan.offs[plan.input])
-    arena[o:o + img.size] = img.ravel()
-    gpu = H.Gpu(plan)
-    gpu.begin(img)
-    worst = {}
-    failures = []
-    for i, op in enumerate(plan.ops):
-        for s in op_sources(plan, op):
-            gpu.write_buf(s, buf(plan, arena, s))
-        gpu.step_op(i)
-        O.step(plan, arena, i)
-        ok, key, rel = judge_op(plan, arena, op, gpu.read_buf(op.dst))
-        worst[key] = max(worst.get(key, 0.0), rel)
-        if not ok:
-            failures.append("op %d %s: %s %.3g" % (i, op.describe(), "differs" if key in EXACT else "err", rel))
-    report(worst)
-    gpu.close()
-    return failures
+    r = D.verify_walk(plan, img, O.step, judge=judge_op, resync=True, max_report=40)
+    report(r["worst_by_key"])
+    return ["op %d %s: %s %.3g" % (f["op"], f["describe"], "differs" if f["key"] in EXACT else "err",
+                                   f["relative"]) for f in r["failures"]]
 
 
 @pytest.mark.parametrize("variant,h,w", [("S-2", 64, 64), ("S-3", 128, 192)])
@@ -66,3 +52,35 @@ def test_unscaled_he_normal_ops(gpu_ok):
     img = np.random.default_rng(5).random((3, 64, 64), dtype=np.float32)
     failures = walk(plan, img, lambda wst: print("worst per kind:", {k: "%.3g" % v for k, v in sorted(wst.items())}))
     assert not failures, "\n".join(failures[:40])
+
+
+def test_reference_verify_walk(gpu_ok):
+    """The reference's own walk (src/main.rs:672-730): both backends step
+    independently from the same image, every op's destination within 1e-3 *
+    max|cpu| (src/main.rs:709-712)."""
+    from maxim_amd import devtools as D
+    from maxim_amd import plan as P
+    from oracle import oracle as O
+    plan = P.Plan(weights("S-3"), 64, 64)
+    r = D.verify_walk(plan, smooth_image(64, 64, seed=6), O.step, out=print)
+    assert r["ops"] == 2885 and r["bad"] == 0, r["failures"][:5]
+
+
+def test_verify_walk_names_the_first_wrong_op(gpu_ok):
+    """A mistake planted in the CPU path's op 700 (its destination shifted by
+    1e-2 of its scale) is the walk's first failure, with its element."""
+    from maxim_amd import devtools as D
+    from maxim_amd import plan as P
+    from oracle import oracle as O
+    plan = P.Plan(weights("S-2"), 64, 64)
+    bad_op = 700
+
+    def planted(pl, arena, i):
+        O.step(pl, arena, i)
+        if i == bad_op:
+            o = int(pl.offs[pl.ops[i].dst])
+            seg = arena[o:o + pl.buf_len(pl.ops[i].dst)]
+            seg[17] += 1e-2 * max(float(np.abs(seg).max()), 1e-3)
+
+    r = D.verify_walk(plan, smooth_image(64, 64, seed=6), planted)
+    assert r["bad"] >= 1 and r["first"]["op"] == bad_op and r["first"]["element"] == 17, r["first"]
