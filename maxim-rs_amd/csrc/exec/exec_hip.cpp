@@ -469,10 +469,31 @@ public:
                 for (auto &l : st.launches) launch(const_cast<Launch &>(l));
                 launched += st.last - st.first;
             } else {
-                for (uint64_t i = std::max(first, st.first); i < std::min(last, st.last); ++i) run_op(i);
+                // A step the range cuts runs its ops one by one, each with its
+                // own launch, reading what the earlier ops of the step left in
+                // the arena (a contiguous run continues where the previous one
+                // stopped). An elided forward permutation's output was never
+                // written, as its readers take the source through a map when
+                // they run fused: a reader run on its own gets it restored
+                // first, from the source, which is intact until the step that
+                // rewrites it has finished.
+                std::set<int64_t> restored;
+                for (uint64_t i = std::max(first, st.first); i < std::min(last, st.last); ++i) {
+                    for (int64_t b : op_srcs[i]) {
+                        auto it = elided_perm.find(b);
+                        if (b < 0 || it == elided_perm.end() || it->second >= i || restored.count(b)) continue;
+                        for (auto &l : ops[it->second]) launch(l);
+                        restored.insert(b);
+                    }
+                    run_op(i);
+                }
             }
         }
     }
+    // The sources each op reads (a resize's intermediate plane excluded), and
+    // each elided forward permutation's output -> its op.
+    std::vector<std::array<int64_t, 2>> op_srcs;
+    std::map<int64_t, uint64_t> elided_perm;
     std::vector<Step> prog;
     // The fused program with every scratch pointer in the code object's
     // static scratch (empty when this plan needs more than it holds).
@@ -731,6 +752,9 @@ Gpu::Gpu(const mx_plan_desc *p) : H(hip()), doff(pg.doff) {
 
 void Gpu::init(const mx_plan_desc *p) {
     validate(p);
+    op_srcs.assign(p->n_ops, {-1, -1});
+    for (uint64_t i = 0; i < p->n_ops; ++i)
+        op_srcs[i] = {p->ops[i].src, p->ops[i].kind == MX_OP_RESIZE ? -1 : p->ops[i].src2};
     check(H.hipInit(0), "hipInit");
     int ndev = 0;
     check(H.hipGetDeviceCount(&ndev), "hipGetDeviceCount");
@@ -1349,6 +1373,17 @@ void Program::plan_fusion(const mx_plan_desc *p, bool require_clear) {
         return R{p->offs[id], p->offs[id] + (uint64_t)(s.c * s.h * s.w)};
     };
     auto overlap = [](R x, R y) { return x.a < y.b && y.a < x.b; };
+    // Whether buffer `id` must stay intact to the end of a pass (a named
+    // dump): the plan marks the storage owner, so a view is kept when its
+    // root (following alias_parent) is.
+    auto kept = [&](int64_t id) {
+        if (!p->keep || id < 0) return false;
+        for (int guard = 0; id >= 0 && guard < 64; ++guard) {
+            if (p->keep[id]) return true;
+            id = p->alias_parent ? p->alias_parent[id] : -1;
+        }
+        return false;
+    };
     auto reads_of = [&](const mx_op &o) {
         std::vector<int64_t> v{o.src};
         if (o.src2 >= 0 && o.kind != MX_OP_RESIZE) v.push_back(o.src2);
@@ -1519,7 +1554,7 @@ void Program::plan_fusion(const mx_plan_desc *p, bool require_clear) {
             if (x == d || base[x] != x || (!views[x] && writers[x] != 1) || (views[x] && writers[x]) || target[x] ||
                 elide_to[d] >= 0 || elide_to[x] >= 0)  // x copied twice: it takes the first destination only
                 continue;
-            if ((uint64_t)x == p->input || (uint64_t)x == p->output || (p->keep && p->keep[x])) continue;
+            if ((uint64_t)x == p->input || (uint64_t)x == p->output || kept(x)) continue;
             if ((uint64_t)c.n != blen(x) || (uint64_t)c.n != blen(d)) continue;
             bool ok = true;
             // w: x's writer, or the first writer of one of its views; every
@@ -1697,7 +1732,7 @@ void Program::plan_fusion(const mx_plan_desc *p, bool require_clear) {
         const uint64_t n = (uint64_t)(q.c * q.h * q.wd);
         if (q.p[0] * q.p[2] != q.h || q.p[1] * q.p[3] != q.wd || q.p[3] % 4 || q.wd % 4 || n >= (1ULL << 31)) continue;
         if (range(P).b - range(P).a != n || range(S).b - range(S).a != n || overlap(range(P), range(S))) continue;
-        if ((uint64_t)P == p->output || (p->keep && p->keep[P])) continue;
+        if ((uint64_t)P == p->output || kept(P)) continue;
         StepSpec &J = specs[spec_of[j]];
         if (J.first != j || J.last != j + 1 || J.rule != RULE_NONE) continue;
         // A GateMm straight on P (the cross-gating blocks): its X is P's
@@ -1775,7 +1810,7 @@ void Program::plan_fusion(const mx_plan_desc *p, bool require_clear) {
                 if (clear_of(ln.dst, reads) && !overlap(range(ln.dst), lr)) {
                     sp.lno = (int64_t)L.first;
                     sp.lno_keep = !only_reader(ln.src, L.first - 1, L.first) || (uint64_t)ln.src == p->output ||
-                                  (uint64_t)y == p->output || (p->keep && (p->keep[ln.src] || p->keep[y]));
+                                  (uint64_t)y == p->output || kept(ln.src) || kept(y);
                     sp.last = L.last;
                     ++fused_ops;
                     ++s;
@@ -2378,6 +2413,11 @@ void Gpu::build_program(const mx_plan_desc *p) {
         for (Launch &l : st.launches) specialise(l);
         for (Launch &l : st.pre) specialise(l);
     }
+    elided_perm.clear();
+    for (const Step &st : prog)
+        if (st.launches.empty() && st.last == st.first + 1 && p->ops[st.first].kind == MX_OP_BLOCK_PERM &&
+            !ops[st.first].empty())
+            elided_perm[p->ops[st.first].dst] = st.first;
 }
 
 // A fused streaming kernel (mx_pw_..._f or _f_lo) specialised for the

@@ -166,3 +166,30 @@ def test_graph_replays_match_eager(gpu_ok):
         other = gpu.run(imgs[(k + 1) % 3])
         assert np.array_equal(got.view(np.uint32), eager[k].view(np.uint32)), rep
         assert np.array_equal(other.view(np.uint32), eager[(k + 1) % 3].view(np.uint32)), rep
+
+
+def test_runs_of_ops_that_cut_fused_steps(gpu_ok):
+    """A pass run as contiguous runs of ops (mxh_run_ops), with every cut
+    inside a fused step - among them steps that read an elided forward
+    permutation's output, which then has to be restored - gives the full
+    pass's bits."""
+    from maxim_amd import plan as P
+    from maxim_amd import hip as H
+    plan = P.Plan(weights("S-3"), 64, 64)
+    img = smooth_image(64, 64, seed=13)
+    gpu = H.Gpu(plan)
+    full = gpu.run(img).copy()
+    steps = gpu.steps()
+    perm_steps = {a for a, b, k in steps if b == a + 1 and not k and plan.ops[a].kind == P.BLOCK_PERM}
+    multi = [(a, b) for a, b, k in steps if b - a >= 2]
+    # cut inside every 7th multi-op step, and inside every step right after an elided permutation
+    after_perm = [(a, b) for (a, b) in multi if any(q < a and q + 40 > a for q in perm_steps)]
+    cuts = sorted({(a + b) // 2 for (a, b) in multi[::7] + after_perm[::3]})
+    print("%d steps, %d elided permutations, %d cuts" % (len(steps), len(perm_steps), len(cuts)), flush=True)
+    assert perm_steps and len(cuts) > 20
+    gpu.begin(img)
+    edges = [0] + cuts + [len(plan.ops)]
+    for a, b in zip(edges, edges[1:]):
+        gpu.run_ops(a, b)
+    got = gpu.read_buf(plan.output).reshape(full.shape)
+    assert np.array_equal(got.view(np.uint32), full.view(np.uint32))
