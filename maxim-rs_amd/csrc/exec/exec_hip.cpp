@@ -292,7 +292,50 @@ std::string gemm_name(Tile t, bool vec) {
 struct ConvCfg {
     int bm = 0, th = 0, ck = 0;
     int c3bm = 0, c3th = 0;  // the mx_c3 tile, when the op qualifies for it
+    int wtc = 0;             // the Winograd kernel's tile columns (4 or 8), 0: not eligible
 };
+
+// The Winograd F(2x2, 3x3) kernels (wino.h) take 3x3 convs of at least 8
+// input channels (a multiple of 8) and 32 output channels, in blocks of 32
+// output channels x 4 x TC tiles: TC = 8 (8 x 16 pixels) where that fills
+// the chip four blocks deep, else 4 (8 x 8).
+int pick_wino(int64_t ci, int64_t co, int64_t h, int64_t w, int cus) {
+    if (ci < 8 || ci % 8 || co < 32 || w % 4 || 8 * h * w >= (1LL << 31)) return 0;
+    const int64_t mb = (co + 31) / 32, slots = 4LL * (cus > 0 ? cus : 256);
+    if (w % 16 == 0 && ((h + 7) / 8) * (w / 16) * mb >= slots) return 8;
+    return w % 8 == 0 ? 4 : 0;
+}
+
+// F(2x2, 3x3)'s filter transform U = G g G^T (G = [1 0 0; 1/2 1/2 1/2;
+// 1/2 -1/2 1/2; 0 0 1]) of every (output, input) channel pair, in double and
+// rounded once, laid out per (32-channel output block, 8-channel input
+// chunk) as [wave][lane][16]: wave w holds the transform row xi = w, and lane
+// (k, r) = (lane / 16, lane % 16) its MFMA A operand, value (nu, ks, mi) =
+// U[4 w + nu][channel 8 chunk + 4 ks + k][output 32 block + 16 mi + r].
+std::vector<float> wino_weights(const float *w, int64_t co, int64_t ci) {
+    static const double G[4][3] = {{1, 0, 0}, {0.5, 0.5, 0.5}, {0.5, -0.5, 0.5}, {0, 0, 1}};
+    const int64_t nmb = (co + 31) / 32, nch = (ci + 7) / 8;
+    std::vector<float> out((size_t)(nmb * nch * 4 * 64 * 16), 0.0f);
+    for (int64_t m = 0; m < co; ++m)
+        for (int64_t c = 0; c < ci; ++c) {
+            const float *g = w + (m * ci + c) * 9;
+            double U[4][4];
+            for (int xi = 0; xi < 4; ++xi)
+                for (int nu = 0; nu < 4; ++nu) {
+                    double v = 0.0;
+                    for (int u = 0; u < 3; ++u)
+                        for (int t = 0; t < 3; ++t) v += G[xi][u] * (double)g[u * 3 + t] * G[nu][t];
+                    U[xi][nu] = v;
+                }
+            const int64_t mb = m / 32, mi = (m % 32) / 16, r = m % 16, ch = c / 8, ks = (c % 8) / 4, k = c % 4;
+            for (int xi = 0; xi < 4; ++xi)
+                for (int nu = 0; nu < 4; ++nu) {
+                    const int64_t lane = k * 16 + r, val = (nu * 2 + ks) * 2 + mi;
+                    out[(size_t)((((mb * nch + ch) * 4 + xi) * 64 + lane) * 16 + val)] = (float)U[xi][nu];
+                }
+        }
+    return out;
+}
 
 // The mx_c3 tile (c_in % 16 == 0 and >= 128, width % 4 == 0; measured
 // faster than the implicit-GEMM kernel there, slower below): 64 output
@@ -327,7 +370,7 @@ ConvCfg pick_conv(int64_t co, int64_t ci, int64_t oh, int64_t ow, bool k3, int c
         // measured on MI355X at the MAXIM shapes (c -> c, 32 to 128 channels):
         // 32-channel blocks of 8 rows for narrow outputs, 64 x 4 up to 64
         // channels, 32 x 4 beyond (the grid-filling shapes win)
-        r.bm = co <= 32 ? 32 : co <= 64 ? 64 : 32;
+        r.bm = co <= 16 ? 16 : co <= 32 ? 32 : co <= 64 ? 64 : 32;
         r.th = co <= 32 ? 8 : 4;
     }
     return r;
@@ -843,6 +886,10 @@ void Gpu::init(const mx_plan_desc *p) {
                                     }
                     extra[i][1] = placev(u);
                 }
+                if (k3 && !std::getenv("MAXIM_NO_WINOGRAD")) {
+                    ccfg[i].wtc = pick_wino(o.c_in, o.c_out, o.h, o.wd, cus);
+                    if (ccfg[i].wtc) extra[i][2] = placev(wino_weights(w, o.c_out, o.c_in));
+                }
                 as_is(o.bias);
                 break;
             }
@@ -1119,13 +1166,30 @@ void Gpu::build_launches(const mx_plan_desc *p, const std::vector<int64_t> &woff
                 a.pad_left = (int32_t)(k3 ? 1 : o.p[1]);
                 a.cvec = aligned(a.y, 16) && a.ow % 4 == 0;
                 const ConvCfg &cc = ccfg[i];
-                Launch l = mk(conv_name(cc, k3));
+                // the vector halo fetch: 16-byte aligned input rows and whole
+                // 16-wide tiles
+                const bool xv = k3 && cc.ck == 8 && aligned(a.x, 16) && a.wd % 4 == 0 && a.ow % 16 == 0;
+                std::string cn = conv_name(cc, k3);
+                if (xv) cn = "mx_conv3x3v_" + cn.substr(strlen("mx_conv3x3_"));
+                Launch l = mk(cn);
                 const int64_t tiles = (int64_t)((a.oh + cc.th - 1) / cc.th) * ((a.ow + 15) / 16);
                 l.g[0] = cdiv(tiles, 1);
                 l.g[1] = grid_yz((o.c_out + cc.bm - 1) / cc.bm);
                 set_args(l, a);
                 l.kind = 2;
-                if (k3 && extra[i][1] >= 0 && aligned(a.x, 16) && aligned(a.y, 16)) {
+                if (k3 && cc.wtc && aligned(a.x, 16)) {
+                    // Winograd F(2x2, 3x3): 32 output channels x 4 x TC tiles
+                    ConvArgs b = a;
+                    b.w = X(i, 2);
+                    b.cvec = aligned(a.y, 8) && a.ow % 2 == 0;
+                    Launch q = mk("mx_wino3_t" + std::to_string(cc.wtc));
+                    q.g[0] = cdiv((int64_t)((a.oh + 7) / 8) * ((a.ow + 2 * cc.wtc - 1) / (2 * cc.wtc)), 1);
+                    q.g[1] = grid_yz((o.c_out + 31) / 32);
+                    set_args(q, b);
+                    q.kind = 2;
+                    alt[i].push_back(l);
+                    L.push_back(q);
+                } else if (k3 && extra[i][1] >= 0 && aligned(a.x, 16) && aligned(a.y, 16)) {
                     // mx_c3 (channel-last LDS tiles, 128-bit fragment reads)
                     ConvArgs b = a;
                     b.w = X(i, 1);

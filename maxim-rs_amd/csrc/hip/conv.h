@@ -18,13 +18,25 @@
 
 namespace conv {
 
-template <int BM, int TH, int TW, int CK, int KS, int STRIDE, int WAVES_M, int WAVES_N, bool FUSED>
+// XV (3x3, stride 1, 16-wide tiles, input rows 16-byte aligned and the
+// output a whole number of tiles wide): the halo is fetched as four 128-bit
+// loads per row (the tile's 16 columns) plus the two edge columns, each
+// thread's row, column and channel offsets fixed for the block, and stored
+// in LDS rows of HP = 24 floats with the tile's columns at 4..19 (16-byte
+// aligned), the left edge at 3 and the right edge at 20.
+template <int BM, int TH, int TW, int CK, int KS, int STRIDE, int WAVES_M, int WAVES_N, bool FUSED, bool XV = false>
 __device__ void body(const ConvArgs &a) {
     constexpr int TAPS = KS * KS;
     constexpr int KC = TAPS * CK;
     constexpr int BN = TH * TW;
     constexpr int HH = (TH - 1) * STRIDE + KS, HW = (TW - 1) * STRIDE + KS;
-    constexpr int HALO = CK * HH * HW;
+    static_assert(!XV || (KS == 3 && STRIDE == 1 && TW == 16), "vector halo: 3x3, stride 1, 16 columns");
+    constexpr int HP = XV ? 24 : HW;   // LDS row pitch of the halo
+    constexpr int HC = XV ? 3 : 0;     // LDS column of halo column 0
+    constexpr int HALO = CK * HH * HP;
+    constexpr int NQ = CK * HH * 4;    // XV: 128-bit loads per chunk (four per row)
+    constexpr int NE = CK * HH * 2;    // XV: edge columns per chunk
+    constexpr int NQT = (NQ + 255) / 256;
     constexpr int WTM = BM / WAVES_M, WTN = BN / WAVES_N;
     constexpr int TM = WTM / 16, TN = WTN / 16;
     constexpr int LDM = BM + 4;
@@ -57,28 +69,60 @@ __device__ void body(const ConvArgs &a) {
 #pragma unroll
     for (int j = 0; j < TN; ++j) {
         const int n = wn * WTN + j * 16 + lr;
-        nofs[j] = (n / TW) * STRIDE * HW + (n % TW) * STRIDE;
+        nofs[j] = (n / TW) * STRIDE * HP + (n % TW) * STRIDE + HC;
     }
 
     float4 wr[NW];
-    float hr[NH];
+    float hr[XV ? 1 : NH];
+    // XV: this thread's 128-bit loads (channel c, halo row r, quarter k) and
+    // edge column, as element offsets from the chunk's first channel plane
+    // (-1: outside the image, stored as zeros) and LDS offsets.
+    float4 qr[XV ? NQT : 1];
+    float er = 0.0f;
+    int qoff[XV ? NQT : 1], qlds[XV ? NQT : 1], eoff = -1, elds = 0;
+    if (XV) {
+#pragma unroll
+        for (int i = 0; i < NQT; ++i) {
+            const int q = tid + i * 256, c = q / (HH * 4), r = (q / 4) % HH, k = q % 4, iy = iy0 + r;
+            qoff[i] = (q < NQ && iy >= 0 && iy < a.h) ? c * (int)plane + iy * a.wd + tx0 + 4 * k : -1;
+            qlds[i] = q < NQ ? (c * HH + r) * HP + 4 + 4 * k : -1;
+        }
+        if (tid < NE) {
+            const int c = tid / (HH * 2), r = (tid / 2) % HH, side = tid % 2, iy = iy0 + r;
+            const int ix = side ? tx0 + 16 : tx0 - 1;
+            eoff = (iy >= 0 && iy < a.h && ix >= 0 && ix < a.wd) ? c * (int)plane + iy * a.wd + ix : -1;
+            elds = (c * HH + r) * HP + (side ? 20 : 3);
+        }
+    }
     auto fetch = [&](int chunk) {
         const float4 *src = reinterpret_cast<const float4 *>(wblk + (int64_t)chunk * (KC * BM));
 #pragma unroll
         for (int i = 0; i < NW; ++i)
             if (tid + i * 256 < NW4) wr[i] = src[tid + i * 256];
         const int c0 = chunk * CK;
+        if constexpr (XV) {
+            // CK channels at a time; a chunk past the last channel reads zeros
+            const int cmax = a.ci - c0;
+            const float *xc = a.x + (int64_t)c0 * plane;
 #pragma unroll
-        for (int i = 0; i < NH; ++i) {
-            const int e = tid + i * 256;
-            float v = 0.0f;
-            if (e < HALO) {
-                const int c = e / (HH * HW), r = e % (HH * HW);
-                const int iy = iy0 + r / HW, ix = ix0 + r % HW;
-                if (c0 + c < a.ci && iy >= 0 && iy < a.h && ix >= 0 && ix < a.wd)
-                    v = a.x[(c0 + c) * plane + (int64_t)iy * a.wd + ix];
+            for (int i = 0; i < NQT; ++i) {
+                const int c = (tid + i * 256) / (HH * 4);
+                qr[i] = (qoff[i] >= 0 && c < cmax) ? ld4(xc + qoff[i]) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
             }
-            hr[i] = v;
+            er = (eoff >= 0 && tid / (HH * 2) < cmax) ? xc[eoff] : 0.0f;
+        } else {
+#pragma unroll
+            for (int i = 0; i < NH; ++i) {
+                const int e = tid + i * 256;
+                float v = 0.0f;
+                if (e < HALO) {
+                    const int c = e / (HH * HW), r = e % (HH * HW);
+                    const int iy = iy0 + r / HW, ix = ix0 + r % HW;
+                    if (c0 + c < a.ci && iy >= 0 && iy < a.h && ix >= 0 && ix < a.wd)
+                        v = a.x[(c0 + c) * plane + (int64_t)iy * a.wd + ix];
+                }
+                hr[i] = v;
+            }
         }
     };
 
@@ -89,7 +133,7 @@ __device__ void body(const ConvArgs &a) {
     const float *wl = &Ws[lk][wm * WTM + lr];
     const float *hl[TN];
 #pragma unroll
-    for (int j = 0; j < TN; ++j) hl[j] = Hs + lk * (HH * HW) + nofs[j];
+    for (int j = 0; j < TN; ++j) hl[j] = Hs + lk * (HH * HP) + nofs[j];
 
     f32x4 acc[TM][TN];
 #pragma unroll
@@ -105,17 +149,24 @@ __device__ void body(const ConvArgs &a) {
             const int e = (tid + i * 256) * 4;
             if (e < KC * BM) st4(&Ws[e / BM][e % BM], wr[i]);
         }
+        if constexpr (XV) {
 #pragma unroll
-        for (int i = 0; i < NH; ++i) {
-            const int e = tid + i * 256;
-            if (e < HALO) Hs[e] = hr[i];
+            for (int i = 0; i < NQT; ++i)
+                if (qlds[i] >= 0) st4(Hs + qlds[i], qr[i]);
+            if (tid < NE) Hs[elds] = er;
+        } else {
+#pragma unroll
+            for (int i = 0; i < NH; ++i) {
+                const int e = tid + i * 256;
+                if (e < HALO) Hs[e] = hr[i];
+            }
         }
         __syncthreads();
         if (chunk + 1 < nchunk) fetch(chunk + 1);
         // k = kk + lk: tap kk / CK (CK % 4 == 0), channel kk % CK + lk
 #pragma unroll
         for (int kk = 0; kk < KC; kk += 4) {
-            const int tap = kk / CK, hofs = (kk % CK) * (HH * HW) + (tap / KS) * HW + (tap % KS);
+            const int tap = kk / CK, hofs = (kk % CK) * (HH * HP) + (tap / KS) * HP + (tap % KS);
             float af[TM], bf[TN];
 #pragma unroll
             for (int i = 0; i < TM; ++i) af[i] = wl[kk * LDM + i * 16];
@@ -189,6 +240,22 @@ __device__ void body(const ConvArgs &a) {
     extern "C" __global__ __launch_bounds__(256) void mx_conv3x3_m##BM##_t##TH##SUF##_f(ConvArgs a) { \
         conv::body<BM, TH, 16, CK, 3, 1, WM, WN, true>(a);                                        \
     }
+// mx_conv3x3v_m<BM>_t<TH>[_f]: the same with the vector halo fetch (XV).
+#define MXK_CONV3V(BM, TH, WM, WN)                                                                 \
+    extern "C" __global__ __launch_bounds__(256) void mx_conv3x3v_m##BM##_t##TH(ConvArgs a) {       \
+        conv::body<BM, TH, 16, 8, 3, 1, WM, WN, false, true>(a);                                   \
+    }                                                                                             \
+    extern "C" __global__ __launch_bounds__(256) void mx_conv3x3v_m##BM##_t##TH##_f(ConvArgs a) {   \
+        conv::body<BM, TH, 16, 8, 3, 1, WM, WN, true, true>(a);                                    \
+    }
+MXK_CONV3V(16, 8, 1, 4)
+MXK_CONV3V(32, 8, 1, 4)
+MXK_CONV3V(64, 8, 2, 2)
+MXK_CONV3V(128, 8, 2, 2)
+MXK_CONV3V(32, 4, 2, 2)
+MXK_CONV3V(64, 4, 2, 2)
+MXK_CONV3V(128, 4, 4, 1)
+MXK_CONV3(16, 8, 8, 1, 4, )
 MXK_CONV3(32, 8, 8, 1, 4, )
 MXK_CONV3(64, 8, 8, 2, 2, )
 MXK_CONV3(128, 8, 8, 2, 2, )

@@ -4,6 +4,7 @@
 #include "gemm.h"
 #include "conv.h"
 #include "conv3.h"
+#include "wino.h"
 #include "pointwise.h"
 
 // The scratch of mxh_run_noalloc (channel-mean partial sums and LayerNorm

@@ -1,11 +1,21 @@
-"""Edge shapes of the channel-last 3x3 convolution (mx_c3_*, used from 128
-input channels) against the CPU oracle: image sides that are not a multiple
-of the tile (16 columns, 2, 4 or 8 rows), output-channel counts that leave a
-partial block, 128 and 256 input channels, a fused leaky ReLU, and the
-fallbacks to the implicit-GEMM kernel (fewer input channels; a misaligned
-output).
+"""Edge shapes of the 3x3 convolutions against the CPU oracle: the Winograd
+F(2x2, 3x3) kernel (mx_wino3_*, from 8 input channels in multiples of 8 and
+32 output channels, widths a multiple of 8), the channel-last kernel (mx_c3_*,
+from 128 input channels) and the implicit-GEMM kernel (the rest): image sides
+that are not a multiple of the tile, output-channel counts that leave a
+partial block, channel counts that leave a partial chunk, both Winograd tile
+widths, a fused leaky ReLU, and a misaligned output.
 GEMM bar: max|d| <= 1e-4 * max|cpu| (matrix-core reduction order).
 """
+
+
+def expect_kernel(ci, co, h, w):
+    """The executor's choice of 3x3 kernel for an aligned input."""
+    if ci >= 8 and ci % 8 == 0 and co >= 32 and w % 8 == 0:
+        return "mx_wino3_t8" if w % 16 == 0 and ((h + 7) // 8) * (w // 16) * ((co + 31) // 32) >= 1024 else "mx_wino3_t4"
+    if ci % 16 == 0 and ci >= 128:
+        return "mx_c3_"
+    return "mx_conv3x3v_" if w % 16 == 0 else "mx_conv3x3_"
 
 import numpy as np
 import pytest
@@ -22,7 +32,14 @@ pytestmark = pytest.mark.gpu
     (256, 64, 7, 12),    # sixteen chunks, a 12-wide image
     (128, 64, 33, 4),    # a 4-wide image
     (32, 40, 17, 36),    # below 128 input channels: the implicit-GEMM kernel
-    (24, 16, 8, 16),     # 24 input channels: the implicit-GEMM kernel
+    (24, 16, 8, 16),     # 24 input channels: the implicit-GEMM kernel (vector halo)
+    (32, 32, 19, 48),    # vector halo: ragged rows, three column tiles, every border
+    (20, 40, 13, 32),    # vector halo: a partial channel chunk and a partial block
+    (64, 3, 10, 64),     # three output channels: 16-channel blocks
+    (16, 64, 11, 40),    # Winograd: two chunks, two output blocks, ragged rows
+    (24, 40, 9, 16),     # Winograd: three chunks, a partial output block
+    (32, 32, 128, 1024), # Winograd with 8 x 16-pixel blocks
+    (128, 128, 20, 32),  # Winograd over 16 chunks
 ])
 def test_conv3x3_edges(gpu_ok, ci, co, h, w):
     from maxim_amd import plan as P
@@ -35,7 +52,7 @@ def test_conv3x3_edges(gpu_ok, ci, co, h, w):
     cp = P.CustomPlan([(ci, h, w), (co, h, w)], [op], [wt, b], input=0, output=1)
     got, steps = run_plan(cp, {0: x}, 1)
     print("kernel", steps[0][2])
-    assert steps[0][2].startswith("mx_c3_" if ci % 16 == 0 and ci >= 128 else "mx_conv3x3_")
+    assert steps[0][2].startswith(expect_kernel(ci, co, h, w))
     check(got, O.conv3x3(x, wt, b), "conv3x3 %d->%d @%dx%d" % (ci, co, h, w))
 
 
@@ -58,5 +75,5 @@ def test_conv3x3_lrelu_fused(gpu_ok, misalign):
     got, steps = run_plan(cp, {0: x}, 3)
     print("steps", steps)
     assert len(steps) == 1 and steps[0][2].endswith("_f")
-    assert steps[0][2].startswith("mx_conv3x3_" if misalign else "mx_c3_")
+    assert steps[0][2].startswith("mx_wino3_")
     check(got, oracle_plan(cp, {0: x}, 3), "conv3x3 + lrelu, output misaligned %d" % misalign)
