@@ -886,6 +886,14 @@ void Gpu::init(const mx_plan_desc *p) {
                                     }
                     extra[i][1] = placev(u);
                 }
+                if (k3 && o.c_out <= 4) {
+                    // the vector-ALU kernel's [c_in][9 taps][4] (zero past c_out)
+                    std::vector<float> q((size_t)(o.c_in * 36), 0.0f);
+                    for (int64_t c = 0; c < o.c_in; ++c)
+                        for (int tp = 0; tp < 9; ++tp)
+                            for (int64_t m = 0; m < o.c_out; ++m) q[(c * 9 + tp) * 4 + m] = w[(m * o.c_in + c) * 9 + tp];
+                    extra[i][3] = placev(q);
+                }
                 if (k3 && !std::getenv("MAXIM_NO_WINOGRAD")) {
                     ccfg[i].wtc = pick_wino(o.c_in, o.c_out, o.h, o.wd, cus);
                     if (ccfg[i].wtc) extra[i][2] = placev(wino_weights(w, o.c_out, o.c_in));
@@ -1177,7 +1185,19 @@ void Gpu::build_launches(const mx_plan_desc *p, const std::vector<int64_t> &woff
                 l.g[1] = grid_yz((o.c_out + cc.bm - 1) / cc.bm);
                 set_args(l, a);
                 l.kind = 2;
-                if (k3 && cc.wtc && aligned(a.x, 16)) {
+                if (k3 && o.c_out <= 4 && o.c_in >= 64) {
+                    // at most four outputs from many inputs: the vector-ALU
+                    // kernel (measured faster than 16-channel MFMA blocks
+                    // from 64 inputs at the MAXIM shapes, slower at 32)
+                    ConvArgs b = a;
+                    b.w = X(i, 3);
+                    Launch q = mk("mx_conv3x3_co4");
+                    q.g[0] = cdiv((int64_t)((a.oh + 7) / 8) * ((a.ow + 7) / 8), 1);
+                    set_args(q, b);
+                    q.kind = 2;
+                    alt[i].push_back(l);
+                    L.push_back(q);
+                } else if (k3 && cc.wtc && aligned(a.x, 16)) {
                     // Winograd F(2x2, 3x3): 32 output channels x 4 x TC tiles
                     ConvArgs b = a;
                     b.w = X(i, 2);

@@ -281,3 +281,82 @@ MXK_CONV4(128, 8, 2, 2)
 MXK_CONV4(32, 4, 2, 2)
 MXK_CONV4(64, 4, 2, 2)
 MXK_CONV4(128, 4, 4, 1)
+
+// 3x3 pad 1 with at most four output channels (the stage outputs to RGB): on
+// the vector ALUs, where an MFMA tile would be 3/16 useful. A block owns an
+// 8 x 8 output tile; its four waves split the input channels (wave w takes
+// c = w, w + 4, ...), each staging its channel's 10 x 10 halo in its own LDS
+// rows (no block barrier) with the next channel's halo already in registers,
+// and each lane accumulates its pixel's outputs (weights are wave-uniform,
+// read through the scalar cache); the four partial sums are added in LDS in
+// a fixed order (wave 0 + 1 + 2 + 3), then bias and the epilogue.
+namespace conv {
+
+template <bool FUSED>
+__device__ void co4(const ConvArgs &a) {
+    __shared__ float halo[4][100];
+    __shared__ float part[4][4][64];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int tiles_x = (a.wd + 7) / 8;
+    const int ty0 = (blockIdx.x / tiles_x) * 8, tx0 = (blockIdx.x % tiles_x) * 8;
+    const int py = lane / 8, px = lane % 8;
+    const int64_t plane = (int64_t)a.h * a.wd;
+    // the halo elements this lane stages: e = lane and lane + 64 (< 100)
+    int hoff[2];
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+        const int e = lane + 64 * k, iy = ty0 - 1 + e / 10, ix = tx0 - 1 + e % 10;
+        hoff[k] = (e < 100 && iy >= 0 && iy < a.h && ix >= 0 && ix < a.wd) ? iy * a.wd + ix : -1;
+    }
+    auto fetch = [&](int c, float *r) {
+#pragma unroll
+        for (int k = 0; k < 2; ++k) r[k] = (c < a.ci && hoff[k] >= 0) ? a.x[c * plane + hoff[k]] : 0.0f;
+    };
+    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    float cur[2], nxt[2];
+    fetch(wave, cur);
+    for (int c = wave; c < a.ci; c += 4) {
+        fetch(c + 4, nxt);
+        halo[wave][lane] = cur[0];
+        if (lane < 36) halo[wave][lane + 64] = cur[1];
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        const float *w = a.w + (int64_t)c * 36;  // [c][tap][4]: wave-uniform
+#pragma unroll
+        for (int tap = 0; tap < 9; ++tap) {
+            const float xv = halo[wave][(py + tap / 3) * 10 + px + tap % 3];
+#pragma unroll
+            for (int o = 0; o < 4; ++o) acc[o] = __builtin_fmaf(w[tap * 4 + o], xv, acc[o]);
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        cur[0] = nxt[0];
+        cur[1] = nxt[1];
+    }
+#pragma unroll
+    for (int o = 0; o < 4; ++o) part[o][wave][lane] = acc[o];
+    __syncthreads();
+    if (wave != 0) return;
+    const int oy = ty0 + py, ox = tx0 + px;
+    if (oy >= a.oh || ox >= a.ow) return;
+    for (int o = 0; o < a.co; ++o) {
+        float v = part[o][0][lane];
+        v = v + part[o][1][lane];
+        v = v + part[o][2][lane];
+        v = v + part[o][3][lane];
+        if (a.bias) v = a.bias[o] + v;
+        const int64_t idx = o * (int64_t)a.oh * a.ow + (int64_t)oy * a.ow + ox;
+        if (FUSED) v = epilogue(a.e, v, idx);
+        a.y[idx] = v;
+    }
+}
+
+}  // namespace conv
+
+// mx_conv3x3_co4[_f]: 3x3 pad 1 to at most four output channels (weights
+// [c_in][9][4], zero beyond c_out), one 8 x 8 output tile per block.
+extern "C" __global__ __launch_bounds__(256) void mx_conv3x3_co4(ConvArgs a) { conv::co4<false>(a); }
+extern "C" __global__ __launch_bounds__(256) void mx_conv3x3_co4_f(ConvArgs a) { conv::co4<true>(a); }

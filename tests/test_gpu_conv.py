@@ -11,6 +11,8 @@ GEMM bar: max|d| <= 1e-4 * max|cpu| (matrix-core reduction order).
 
 def expect_kernel(ci, co, h, w):
     """The executor's choice of 3x3 kernel for an aligned input."""
+    if co <= 4 and ci >= 64:
+        return "mx_conv3x3_co4"
     if ci >= 8 and ci % 8 == 0 and co >= 32 and w % 8 == 0:
         return "mx_wino3_t8" if w % 16 == 0 and ((h + 7) // 8) * (w // 16) * ((co + 31) // 32) >= 1024 else "mx_wino3_t4"
     if ci % 16 == 0 and ci >= 128:
@@ -35,7 +37,9 @@ pytestmark = pytest.mark.gpu
     (24, 16, 8, 16),     # 24 input channels: the implicit-GEMM kernel (vector halo)
     (32, 32, 19, 48),    # vector halo: ragged rows, three column tiles, every border
     (20, 40, 13, 32),    # vector halo: a partial channel chunk and a partial block
-    (64, 3, 10, 64),     # three output channels: 16-channel blocks
+    (64, 3, 10, 64),     # three output channels: the vector-ALU kernel
+    (70, 3, 13, 21),     # the same with ragged tiles and a channel count off the wave split
+    (30, 3, 13, 21),     # three outputs from fewer inputs: 16-channel MFMA blocks
     (16, 64, 11, 40),    # Winograd: two chunks, two output blocks, ragged rows
     (24, 40, 9, 16),     # Winograd: three chunks, a partial output block
     (32, 32, 128, 1024), # Winograd with 8 x 16-pixel blocks
