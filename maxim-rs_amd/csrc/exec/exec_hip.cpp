@@ -1001,6 +1001,10 @@ void Gpu::init(const mx_plan_desc *p) {
     check(H.hipMalloc(&ptr, scratch_len * 4), "hipMalloc(scratch)");
     scratch = static_cast<float *>(ptr);
     if (wbytes) check(H.hipMemcpy(wdev, blob.data(), wbytes, kMemcpyH2D), "hipMemcpy(weights)");
+    if (std::getenv("MAXIM_LOG_ALLOC"))
+        fprintf(stderr, "maxim: arena [%p, %p) weights [%p, %p) scratch [%p, %p) static scratch [%p, %p)\n",
+                (void *)arena, (void *)(arena + arena_len), (void *)wdev, (void *)(wdev + wbytes), (void *)scratch,
+                (void *)(scratch + scratch_len), (void *)dc.scratch, (void *)((char *)dc.scratch + dc.scratch_bytes));
 
     build_launches(p, woff, extra, maxt);
     build_program(p);

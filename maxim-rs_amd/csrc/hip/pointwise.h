@@ -68,9 +68,9 @@ __device__ __forceinline__ uint32_t unblock(const BlockMap &q, uint32_t e) {
 // set from the argument block at run time (every combination, one kernel).
 enum { EP_U = 1, EP_R1 = 2, EP_R2 = 4, EP_GELU = 8, EP_LRELU = 16, EP_YMAP = 32, EP_BIAS = 64, EP_R1MAP = 128 };
 
-// LN: 0 no folded LayerNorm; 1 the LayerNorm's full expression on X
-// ((x - m) r w + c, w and c per input channel); 2 its scale and bias
-// already folded into the weights and bias by the host ((x - m) r only).
+// LN: 0 no folded LayerNorm; 1 the LayerNorm's expression on X,
+// (x - m) r w + c with w and c per input channel, in the LayerNorm kernels'
+// order (folding w and c into the weights changes the rounding).
 template <int LAYOUT, int TMW, int KS, bool FUSED, int LN, bool XM = false, bool XMUL = false, bool CT = false,
           bool LNO = false, int EP = -1>
 __device__ void body(const GemmArgs &a) {
@@ -191,16 +191,6 @@ __device__ void body(const GemmArgs &a) {
         }
     };
     auto norm = [&](float4 *xv, const float4 *lv) {
-        if (LN == 2) {
-#pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                xv[q].x = (xv[q].x - lmean.x) * lrstd.x;
-                xv[q].y = (xv[q].y - lmean.y) * lrstd.y;
-                xv[q].z = (xv[q].z - lmean.z) * lrstd.z;
-                xv[q].w = (xv[q].w - lmean.w) * lrstd.w;
-            }
-            return;
-        }
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
             const float w = comp(lv[0], q), c = comp(lv[1], q);
@@ -615,10 +605,3 @@ MXK_PW_E(mx_pw_ch2_k4_mul_f, CH, 2, 4, 0, false, true, false, 66)
 MXK_PW_E(mx_pw_ch2_k4_mul_f, CH, 2, 4, 0, false, true, false, 70)
 MXK_PW_E(mx_pw_rw2_k4_f, RW, 2, 4, 0, false, false, false, 65)
 MXK_PW_E(mx_pw_rw4_k4_f, RW, 4, 4, 0, false, false, false, 65)
-MXK_PW_E(mx_pw_ch2_lnf_f_lo, CH, 2, 1, 2, false, false, true, 72)
-MXK_PW_E(mx_pw_ch2_lnf_f, CH, 2, 1, 2, false, false, false, 72)
-MXK_PW_E(mx_pw_ch2_k4_lnf_f, CH, 2, 4, 2, false, false, false, 72)
-MXK_PW_E(mx_pw_ch1_ln_f, CH, 1, 1, 1, false, false, false, 72)
-MXK_PW_E(mx_pw_ch1_lnf_f, CH, 1, 1, 2, false, false, false, 72)
-MXK_PW_E(mx_pw_ch4_ln_f_lo, CH, 4, 1, 1, false, false, true, 72)
-MXK_PW_E(mx_pw_ch4_ln_f, CH, 4, 1, 1, false, false, false, 72)
