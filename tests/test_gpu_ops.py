@@ -66,6 +66,20 @@ def test_reference_verify_walk(gpu_ok):
     assert r["ops"] == 2885 and r["bad"] == 0, r["failures"][:5]
 
 
+def test_reference_verify_walk_at_c4(gpu_ok):
+    """The same walk at the headline size (MAXIM-3S, 448x640 padded): every
+    tile, split and XCD choice the executor makes there, op by op, within
+    the reference's bar (about 40 s)."""
+    from maxim_amd import devtools as D
+    from maxim_amd import plan as P
+    from oracle import oracle as O
+    plan = P.Plan(weights("S-3"), 448, 640)
+    print("walk S-3 448x640, %d ops" % len(plan.ops), flush=True)
+    r = D.verify_walk(plan, smooth_image(448, 640, seed=6), O.step, out=print)
+    assert r["ops"] == 2885 and r["bad"] == 0, r["failures"][:5]
+    assert r["worst"] < 1e-4, r["worst"]
+
+
 def test_verify_walk_names_the_first_wrong_op(gpu_ok):
     """A mistake planted in the CPU path's op 700 (its destination shifted by
     1e-2 of its scale) is the walk's first failure, with its element."""
