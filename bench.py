@@ -133,7 +133,7 @@ def main():
     # (launch_costs).
     steps = gpu.steps()
     launches = gpu.launches()
-    cost = launch_costs(plan, steps, launches, R)
+    cost = launch_costs(plan, steps, launches, R, gpu.launch_spans())
     per_kernel = collections.defaultdict(lambda: [0.0, 0, 0.0, 0.0])  # ms, launches, flops, bytes
     ev_tot = []
     for _ in range(args.steps):
@@ -270,7 +270,7 @@ def c5_leg(w, R, steps=3):
         gpu.sync()
         ms = (time.perf_counter() - t0) * 1e3 / steps
         launches = gpu.launches()
-        cost = launch_costs(plan, gpu.steps(), launches, R)
+        cost = launch_costs(plan, gpu.steps(), launches, R, gpu.launch_spans())
         _, tot = gpu.run_timed()
         lt = gpu.launch_timeline()
         per = collections.defaultdict(lambda: [0.0, 0, 0.0, 0.0])
@@ -322,11 +322,14 @@ def traffic_per_launch(kernel):
     return None
 
 
-def launch_costs(plan, steps, launches, R):
+def launch_costs(plan, steps, launches, R, spans=None):
     """(flops, bytes) of every launch: FLOPs = 2 x MACs; bytes = what the
     kernel must move (inputs once, output once, weights once). A step of one
     launch is charged its ops' costs less the intermediates it no longer
-    writes and reads back; the steps of several launches are split by kernel:
+    writes and reads back; a launch that names its own ops (`spans`: in a
+    step pairing two branches' launches, each launch computes one former
+    step, or two side by side) is charged as those steps were; the other
+    steps of several launches are split by kernel:
     a folded LayerNorm's statistics pass (reads x, writes mean and 1/std) and
     the GEMM that re-reads x with them, the two resize passes through `tmp`,
     the channel mean's partial and final sums, and the partial sums before
@@ -368,6 +371,15 @@ def launch_costs(plan, steps, launches, R):
         a, b, _ = steps[st]
         o = plan.ops[a]
         names = [launches[i][1] for i in idx]
+        if spans is not None and any(spans[i][1] is not None or spans[i][0] != (a, b) for i in idx):
+            for i in idx:
+                (a0, b0), second = spans[i]
+                f, by = step_cost(a0, b0)
+                if second is not None:
+                    f2, by2 = step_cost(*second)
+                    f, by = f + f2, by + by2
+                out[i] = (f, by)
+            continue
         if len(idx) == 1:
             out[idx[0]] = step_cost(a, b)
             continue

@@ -133,6 +133,12 @@ int mxh_run_timed(mxh_gpu *g, const mx_plan_desc *plan);
  * sum over its launches. */
 uint64_t mxh_launches(mxh_gpu *g);
 int mxh_launch_info(mxh_gpu *g, uint64_t i, uint64_t *step, const char **kernel);
+/* The ops launch i computes: ops[0..1] the first range [first, last), and
+ * for a launch that runs two steps' work side by side (a step pairing the
+ * grid and block branches of a multi-axis gMLP block) ops[2..3] the second,
+ * else 0, 0. No counterpart in the reference (one launch per op there); it
+ * lets a profile charge each launch its own ops. */
+int mxh_launch_span(mxh_gpu *g, uint64_t i, uint64_t ops[4]);
 int mxh_launch_timeline(mxh_gpu *g, float *ms, uint64_t n);
 
 /* Time `iters` passes of ops [first, last) back to back with HIP events on

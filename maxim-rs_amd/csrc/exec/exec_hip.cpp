@@ -86,10 +86,14 @@ struct Launch {
     unsigned g[3] = {1, 1, 1};
     unsigned b[3] = {MXK_BLOCK, 1, 1};
     unsigned shm = 0;  // dynamic LDS bytes
-    alignas(16) unsigned char a0[384];
+    alignas(16) unsigned char a0[736];
     alignas(16) unsigned char a1[32];
     int nparams = 1;
-    int kind = 0;  // 1: a0 holds GemmArgs (plain epilogue), 2: ConvArgs
+    int kind = 0;  // 1: a0 holds GemmArgs (plain epilogue), 2: ConvArgs, 3: DualGemmArgs
+    // The ops this launch computes when its step pairs launches of several
+    // former steps: [span[0], span[1]), and for a paired launch also
+    // [span[2], span[3]); all zero: the whole step's ops.
+    uint64_t span[4] = {0, 0, 0, 0};
 };
 
 // A run of ops [first, last) executed by `launches`: one op's own launches,
@@ -426,7 +430,14 @@ struct Program {
     uint64_t fused_ops = 0;
     uint64_t so_len = 0;  // floats of the LayerNorm statistics region
     bool repacked = false;
+    // Runs of steps (spec index ranges, inclusive) holding two steps of the
+    // same shape that touch disjoint memory - the grid and block branches of a
+    // multi-axis gMLP block - whose buffers the layout keeps apart for the
+    // whole run, so that their launches may share one grid.
+    std::vector<std::pair<uint64_t, uint64_t>> regions;
     void plan_fusion(const mx_plan_desc *p, bool require_clear);
+    void storage(const mx_plan_desc *p, std::vector<int64_t> &base, std::vector<uint64_t> &delta) const;
+    void plan_regions(const mx_plan_desc *p);
     void layout(const mx_plan_desc *p, bool repack);
 };
 
@@ -547,6 +558,7 @@ public:
     uint64_t plan_arena_len = 0;
     void build_program(const mx_plan_desc *p);
     void specialise(Launch &l);
+    void pair_launches(const mx_plan_desc *p);
     void sync() { check(H.hipStreamSynchronize(stream), "hipStreamSynchronize"); }
     // All ops with an event before each and one after the last; one sync.
     // Every step (one op, or one fused launch standing for several) with an
@@ -949,6 +961,7 @@ void Gpu::init(const mx_plan_desc *p) {
     plan_arena_len = p->arena_len;
     const bool repack = p->alias_parent && p->alias_delta && !std::getenv("MAXIM_PLAN_LAYOUT");
     pg.plan_fusion(p, !repack);
+    if (repack && !std::getenv("MAXIM_NO_PAIR")) pg.plan_regions(p);
     pg.layout(p, repack);
     arena_len = pg.arena_len;
     // A 1x1 conv whose step normalises (or takes the statistics of) output
@@ -2015,6 +2028,126 @@ void Program::plan_fusion(const mx_plan_desc *p, bool require_clear) {
 // a fused step - the eliminated intermediate included, which the unfused path
 // still writes - is live at once and no two of them share storage. Views keep
 // their delta inside their parent; kept (named) buffers live to the end.
+// The buffer that owns every buffer's storage and its offset there: views
+// sit in their parents, an elided copy's source (with the views inside it)
+// takes its destination's storage, which may itself sit on another's.
+void Program::storage(const mx_plan_desc *p, std::vector<int64_t> &base, std::vector<uint64_t> &delta) const {
+    const uint64_t n = p->n_bufs;
+    base.assign(n, 0);
+    delta.assign(n, 0);
+    for (uint64_t i = 0; i < n; ++i) {
+        const int64_t par = p->alias_parent[i];
+        if (par < 0) { base[i] = (int64_t)i; delta[i] = 0; }
+        else {
+            if ((uint64_t)par >= i) throw Error("the view table names a later buffer as a parent");
+            base[i] = base[par];
+            delta[i] = delta[par] + p->alias_delta[i];
+        }
+    }
+    std::vector<char> done(n, 0);
+    std::function<void(uint64_t)> resolve = [&](uint64_t i) {
+        if (done[i]) return;
+        done[i] = 1;
+        const int64_t x = base[i];
+        if (x < (int64_t)elide_to.size() && elide_to[x] >= 0) {
+            const int64_t d = elide_to[x];
+            resolve((uint64_t)d);
+            const uint64_t dx = delta[i];  // offset inside x
+            base[i] = base[d];
+            delta[i] = delta[d] + dx;
+        }
+    };
+    for (uint64_t i = 0; i < n; ++i) resolve(i);
+}
+
+// Regions (see `regions`): within a window of at most 12 consecutive steps
+// made only of 1x1-conv/GateMm steps and the pointwise, LayerNorm,
+// permutation and copy ops fused around them, every pair of steps with the
+// same op sequence and shapes (the two branches' steps differ only in how
+// their pixels are blocked, not in their sizes) whose buffers do not meet
+// with a write; the region runs from the first such step to the last.
+void Program::plan_regions(const mx_plan_desc *p) {
+    regions.clear();
+    if (!p->alias_parent || !p->alias_delta) return;
+    constexpr uint64_t W = 12;
+    std::vector<int64_t> base;
+    std::vector<uint64_t> delta;
+    storage(p, base, delta);
+    auto len = [&](int64_t b) { return (uint64_t)(p->bufs[b].c * p->bufs[b].h * p->bufs[b].w); };
+    // (GEMMs over at most 80000 pixels: a full-resolution branch already
+    // fills the chip on its own, and two of its memory-bound launches side
+    // by side measured slower, not faster)
+    auto member = [&](uint64_t s) {
+        bool gemm = false;
+        for (uint64_t k = specs[s].first; k < specs[s].last; ++k) {
+            switch (p->ops[k].kind) {
+                case MX_OP_CONV1X1:
+                    if (p->ops[k].h * p->ops[k].wd > 80000) return 0;
+                    gemm = true;
+                    break;
+                case MX_OP_GATE_MM: gemm = true; break;
+                case MX_OP_GATE_APPLY: case MX_OP_GELU: case MX_OP_ADD: case MX_OP_MUL: case MX_OP_CHAN_LN:
+                case MX_OP_BLOCK_PERM: case MX_OP_COPY: case MX_OP_LRELU: break;
+                default: return 0;
+            }
+        }
+        return gemm ? 2 : 1;  // 2: a step with a GEMM, 1: one that may sit between
+    };
+    auto sig = [&](uint64_t s) {
+        std::vector<int64_t> v;
+        for (uint64_t k = specs[s].first; k < specs[s].last; ++k) {
+            const mx_op &o = p->ops[k];
+            v.insert(v.end(), {(int64_t)o.kind, (int64_t)o.mode, o.c_in, o.c_out, o.h * o.wd, o.n, o.c, o.hw});
+        }
+        return v;
+    };
+    struct Iv { int64_t owner; uint64_t lo, hi; };
+    auto touch = [&](uint64_t s, std::vector<Iv> &rd, std::vector<Iv> &wr) {
+        auto iv = [&](int64_t b) { return Iv{base[b], delta[b], delta[b] + len(b)}; };
+        for (uint64_t k = specs[s].first; k < specs[s].last; ++k) {
+            const mx_op &o = p->ops[k];
+            if (o.dst >= 0) { wr.push_back(iv(o.dst)); rd.push_back(iv(o.dst)); }
+            if (o.src >= 0) rd.push_back(iv(o.src));
+            if (o.src2 >= 0) rd.push_back(iv(o.src2));
+        }
+        for (int64_t b : {specs[s].xsrc, specs[s].r1, specs[s].u, specs[s].r2})
+            if (b >= 0) rd.push_back(iv(b));
+    };
+    auto meets = [](const std::vector<Iv> &x, const std::vector<Iv> &y) {
+        for (const Iv &u : x)
+            for (const Iv &v : y)
+                if (u.owner == v.owner && u.lo < v.hi && v.lo < u.hi) return true;
+        return false;
+    };
+    uint64_t i = 0;
+    const uint64_t S = specs.size();
+    while (i < S) {
+        if (member(i) != 2) { ++i; continue; }
+        uint64_t j = i + 1;
+        while (j < S && j - i < W && member(j)) ++j;
+        std::vector<std::vector<Iv>> rd(j - i), wr(j - i);
+        for (uint64_t s = i; s < j; ++s) touch(s, rd[s - i], wr[s - i]);
+        uint64_t lo = UINT64_MAX, hi = 0;
+        for (uint64_t u = i; u < j; ++u) {
+            if (member(u) != 2) continue;
+            const auto su = sig(u);
+            for (uint64_t v = u + 1; v < j; ++v) {
+                if (member(v) != 2 || sig(v) != su) continue;
+                const size_t a = u - i, b = v - i;
+                if (meets(wr[a], rd[b]) || meets(wr[b], rd[a])) continue;
+                lo = std::min(lo, u);
+                hi = std::max(hi, v);
+            }
+        }
+        if (lo != UINT64_MAX) {
+            regions.push_back({lo, hi});
+            i = hi + 1;
+        } else {
+            i = j;
+        }
+    }
+}
+
 void Program::layout(const mx_plan_desc *p, bool repack) {
     const uint64_t n = p->n_bufs;
     doff.assign(n, 0);
@@ -2030,33 +2163,9 @@ void Program::layout(const mx_plan_desc *p, bool repack) {
         arena_len = p->arena_len;
         return;
     }
-    std::vector<int64_t> base(n);
-    std::vector<uint64_t> delta(n);
-    for (uint64_t i = 0; i < n; ++i) {
-        const int64_t par = p->alias_parent[i];
-        if (par < 0) { base[i] = (int64_t)i; delta[i] = 0; }
-        else {
-            if ((uint64_t)par >= i) throw Error("the view table names a later buffer as a parent");
-            base[i] = base[par];
-            delta[i] = delta[par] + p->alias_delta[i];
-        }
-    }
-    // an elided copy's source (with the views inside it) takes its
-    // destination's storage, which may itself sit on another's
-    std::vector<char> done(n, 0);
-    std::function<void(uint64_t)> resolve = [&](uint64_t i) {
-        if (done[i]) return;
-        done[i] = 1;
-        const int64_t x = base[i];
-        if (x < (int64_t)elide_to.size() && elide_to[x] >= 0) {
-            const int64_t d = elide_to[x];
-            resolve((uint64_t)d);
-            const uint64_t dx = delta[i];  // offset inside x
-            base[i] = base[d];
-            delta[i] = delta[d] + dx;
-        }
-    };
-    for (uint64_t i = 0; i < n; ++i) resolve(i);
+    std::vector<int64_t> base;
+    std::vector<uint64_t> delta;
+    storage(p, base, delta);
     for (uint64_t i = 0; i < n; ++i) dbase[i] = base[i];
     const uint64_t DEAD = UINT64_MAX;
     std::vector<uint64_t> first(n, DEAD), last(n, 0);
@@ -2075,6 +2184,27 @@ void Program::layout(const mx_plan_desc *p, bool repack) {
         use(specs[s].xsrc);
         use(specs[s].r1);
     }
+    // every buffer a region touches is live across the whole region, so
+    // that its steps may run in another order or side by side - except the
+    // intermediates only one step touches, which its fused launch never
+    // stores (op by op, the steps run in their own order)
+    const std::vector<uint64_t> first0 = first, last0 = last;
+    for (const auto &rg : regions)
+        for (uint64_t s = rg.first; s <= rg.second; ++s) {
+            auto span = [&](int64_t b) {
+                if (b < 0) return;
+                const int64_t r = base[b];
+                if (first0[r] == last0[r]) return;
+                first[r] = std::min(first[r], rg.first);
+                last[r] = std::max(last[r], rg.second);
+            };
+            for (uint64_t k = specs[s].first; k < specs[s].last; ++k) {
+                const mx_op &o = p->ops[k];
+                for (int64_t b : {o.dst, o.src, o.src2}) span(b);
+            }
+            span(specs[s].xsrc);
+            span(specs[s].r1);
+        }
     if (p->keep)
         for (uint64_t i = 0; i < n; ++i)
             if (p->keep[i] && first[base[i]] != DEAD) last[base[i]] = specs.size() - 1;
@@ -2506,6 +2636,228 @@ void Gpu::build_program(const mx_plan_desc *p) {
         if (st.launches.empty() && st.last == st.first + 1 && p->ops[st.first].kind == MX_OP_BLOCK_PERM &&
             !ops[st.first].empty())
             elided_perm[p->ops[st.first].dst] = st.first;
+    if (!std::getenv("MAXIM_NO_PAIR")) pair_launches(p);
+}
+
+// Pairs of independent streaming-GEMM launches of one kernel within a few
+// steps of each other (the grid and block branches of a multi-axis gMLP
+// block: their in-projections, their out-projections) become one launch of
+// the kernel's _x2 form, so that two grids too small to fill the chip share
+// it and one tail. Within a window of consecutive steps whose launches are
+// all single streaming GEMMs (or none), launches are list-scheduled over the
+// steps' dependencies - any two steps whose device bytes (arena, and the
+// scratch statistics their arguments name) overlap with a write keep their
+// order - taking two ready launches of one kernel together where it can, and
+// otherwise holding back a launch whose partner is still waiting on others.
+// A window in which anything was paired becomes one step over all its ops:
+// every op still computes exactly what it did, in a dependency-respecting
+// order, so results are unchanged to the bit; a run of ops that cuts the
+// window runs its ops one by one.
+void Gpu::pair_launches(const mx_plan_desc *p) {
+    constexpr size_t W = 12;
+    struct Iv {
+        int space;  // 0 arena, 1 scratch
+        uint64_t lo, hi;
+    };
+    auto x2fn = [&](const char *name) -> hipFunction_t {
+        const std::string n = std::string(name) + "_x2";
+        auto it = fns_.find(n);
+        if (it != fns_.end()) return it->second;
+        hipFunction_t f = nullptr;
+        if (H.hipModuleGetFunction(&f, mod, n.c_str()) != 0) f = nullptr;
+        fns_[n] = f;
+        return f;
+    };
+    auto single = [&](const Step &st) {
+        if (st.launches.size() != 1 || st.launches[0].kind != 1) return false;
+        const char *n = st.launches[0].name;
+        const size_t k = strlen(n);
+        return strncmp(n, "mx_pw_", 6) == 0 && !(k > 2 && strcmp(n + k - 2, "_t") == 0);
+    };
+    auto member = [&](const Step &st) { return (st.launches.empty() && st.pre.empty()) || single(st); };
+    // the device memory a step's streaming-GEMM launch reads and writes,
+    // from its arguments: X (and a folded Mul's second factor), the epilogue
+    // operands and the folded LayerNorm's statistics are read; the output and
+    // the output LayerNorm's band (or statistics) are written. Extents are
+    // per batch (a block map permutes within them: X over its plane, Y
+    // within M x N); weights and biases are never written and are left out.
+    auto footprint = [&](const Step &st, std::vector<Iv> &rd, std::vector<Iv> &wr) {
+        const Launch &l = st.launches[0];
+        GemmArgs a;
+        memcpy(&a, l.a0, sizeof a);
+        auto add = [&](std::vector<Iv> &v, const float *q, int64_t stride, uint64_t len) {
+            if (!q || len == 0) return;
+            const uint64_t span = (uint64_t)((a.batch > 1 ? (int64_t)(a.batch - 1) * stride : 0)) + len;
+            if (q >= arena && q < arena + arena_len)
+                v.push_back(Iv{0, (uint64_t)(q - arena), (uint64_t)(q - arena) + span});
+            else if (q >= scratch && q < scratch + scratch_len)
+                v.push_back(Iv{1, (uint64_t)(q - scratch), (uint64_t)(q - scratch) + span});
+        };
+        const bool rw = strncmp(l.name, "mx_pw_rw", 8) == 0;
+        const uint64_t MN = (uint64_t)a.M * (uint64_t)a.N;
+        uint64_t xlen = rw ? (uint64_t)a.M * (uint64_t)a.K : (uint64_t)a.K * (uint64_t)a.N;
+        if (a.xmap.on) xlen = std::max<uint64_t>(xlen, (uint64_t)a.K * (uint64_t)a.xmap.plane);
+        add(rd, a.B, a.sB, xlen);
+        add(rd, a.B2, a.sB, xlen);
+        add(rd, a.e.u, a.sC, MN);
+        add(rd, a.e.r1, a.sC, MN);
+        add(rd, a.e.r2, a.sC, MN);
+        add(rd, a.ln.mean, 0, (uint64_t)a.N);
+        add(rd, a.ln.rstd, 0, (uint64_t)a.N);
+        add(wr, a.C, a.sC, MN);
+        if (a.lo.y) {
+            if (a.lo.mode)
+                add(wr, a.lo.y, 0, (uint64_t)a.lo.nband * 2 * (uint64_t)a.N);
+            else
+                add(wr, a.lo.y, 0, (uint64_t)(a.M - a.lo.row0) * (uint64_t)a.N);
+        }
+    };
+    auto meets = [](const std::vector<Iv> &x, const std::vector<Iv> &y) {
+        for (const Iv &u : x)
+            for (const Iv &v : y)
+                if (u.space == v.space && u.lo < v.hi && v.lo < u.hi) return true;
+        return false;
+    };
+    std::vector<Step> out;
+    out.reserve(prog.size());
+    std::map<size_t, size_t> region_end;  // the layout's regions (steps are its specs here)
+    for (const auto &rg : pg.regions)
+        if (rg.second < prog.size()) region_end[rg.first] = rg.second + 1;
+    size_t i = 0;
+    while (i < prog.size()) {
+        auto rg = region_end.find(i);
+        if (rg == region_end.end()) {
+            out.push_back(std::move(prog[i]));
+            ++i;
+            continue;
+        }
+        // the window: a region whose steps are all single streaming GEMMs (or
+        // launch nothing), with at most one producer of folded-LayerNorm
+        // statistics among their `pre` sources
+        const size_t j = rg->second;
+        int64_t so = -1;
+        bool ok = true;
+        for (size_t k = i; k < j && ok; ++k) {
+            ok = member(prog[k]) && (prog[k].so_from < 0 || so < 0 || prog[k].so_from == so);
+            if (prog[k].so_from >= 0) so = prog[k].so_from;
+        }
+        if (!ok || j - i > W) {
+            for (size_t k = i; k < j; ++k) out.push_back(std::move(prog[k]));
+            i = j;
+            continue;
+        }
+        std::vector<size_t> node;  // window steps with a launch
+        for (size_t k = i; k < j; ++k)
+            if (!prog[k].launches.empty()) node.push_back(k);
+        const size_t m = node.size();
+        std::vector<std::vector<Iv>> rd(m), wr(m);
+        for (size_t u = 0; u < m; ++u) footprint(prog[node[u]], rd[u], wr[u]);
+        std::vector<uint32_t> pred(m, 0), reach(m, 0);
+        for (size_t v = 0; v < m; ++v)
+            for (size_t u = 0; u < v; ++u)
+                if (meets(wr[u], rd[v]) || meets(wr[u], wr[v]) || meets(rd[u], wr[v])) pred[v] |= 1u << u;
+        for (size_t v = 0; v < m; ++v) {
+            reach[v] = pred[v];
+            for (size_t u = 0; u < v; ++u)
+                if (pred[v] >> u & 1) reach[v] |= reach[u];
+        }
+        auto kname = [&](size_t u) { return prog[node[u]].launches[0].name; };
+        if (std::getenv("MAXIM_PAIR_LOG") && m > 1) {
+            fprintf(stderr, "maxim: window steps [%zu, %zu):", i, j);
+            for (size_t u = 0; u < m; ++u) fprintf(stderr, " %zu:%s(g%u/%u, pred %x)", node[u], kname(u), prog[node[u]].launches[0].g[0], prog[node[u]].launches[0].g[1], pred[u]);
+            fprintf(stderr, "\n");
+        }
+        auto one = [&](size_t u) {  // one batch, and a grid that leaves CUs idle
+            const Launch &l = prog[node[u]].launches[0];
+            return l.g[1] == 1 && l.g[2] == 1 && l.g[0] <= (unsigned)(5 * cus);
+        };
+        auto can_pair = [&](size_t u, size_t v) {
+            return kname(u) == kname(v) && one(u) && one(v) && !(reach[v] >> u & 1) && !(reach[u] >> v & 1) &&
+                   x2fn(kname(u)) != nullptr;
+        };
+        // list scheduling: entries are (u) or (u, v)
+        std::vector<std::pair<int, int>> seq;
+        uint32_t done = 0;
+        size_t pairs = 0;
+        while (done != (m == 32 ? 0xffffffffu : (1u << m) - 1)) {
+            std::vector<size_t> ready;
+            for (size_t u = 0; u < m; ++u)
+                if (!(done >> u & 1) && (pred[u] & ~done) == 0) ready.push_back(u);
+            bool paired = false;
+            for (size_t a = 0; a < ready.size() && !paired; ++a)
+                for (size_t b = a + 1; b < ready.size() && !paired; ++b)
+                    if (can_pair(ready[a], ready[b])) {
+                        seq.push_back({(int)ready[a], (int)ready[b]});
+                        done |= (1u << ready[a]) | (1u << ready[b]);
+                        ++pairs;
+                        paired = true;
+                    }
+            if (paired) continue;
+            size_t pick = ready[0];
+            for (size_t u : ready) {
+                bool waits = false;
+                for (size_t w = 0; w < m; ++w)
+                    if (!(done >> w & 1) && w != u && (pred[w] & ~done) != 0 && can_pair(u, w)) waits = true;
+                if (!waits) {
+                    pick = u;
+                    break;
+                }
+            }
+            seq.push_back({(int)pick, -1});
+            done |= 1u << pick;
+        }
+        if (pairs == 0) {
+            for (size_t k = i; k < j; ++k) out.push_back(std::move(prog[k]));
+            i = j;
+            continue;
+        }
+        Step st(prog[i].first, prog[j - 1].last);
+        st.so_from = so;
+        for (size_t k = i; k < j; ++k)
+            for (Launch &l : prog[k].pre) st.pre.push_back(l);
+        for (auto &e : seq) {
+            const Step &sa = prog[node[e.first]];
+            const Launch &a = sa.launches[0];
+            if (e.second < 0) {
+                st.launches.push_back(a);
+                st.launches.back().span[0] = sa.first;
+                st.launches.back().span[1] = sa.last;
+                continue;
+            }
+            const Step &sb = prog[node[e.second]];
+            const Launch &b = sb.launches[0];
+            Launch d = a;
+            d.span[0] = sa.first;
+            d.span[1] = sa.last;
+            d.span[2] = sb.first;
+            d.span[3] = sb.last;
+            d.name = intern(std::string(a.name) + "_x2");
+            d.f = x2fn(a.name);
+            DualGemmArgs da{};
+            memcpy(&da.a, a.a0, sizeof(GemmArgs));
+            memcpy(&da.b, b.a0, sizeof(GemmArgs));
+            da.na = a.g[0];
+            d.g[0] = a.g[0] + b.g[0];
+            d.kind = 3;
+            set_args(d, da);
+            st.main = st.launches.size();
+            st.launches.push_back(d);
+        }
+        out.push_back(std::move(st));
+        i = j;
+    }
+    // step indices of the statistics producers moved with the merging
+    if (out.size() != prog.size()) {
+        std::vector<int64_t> remap(prog.size(), -1);
+        size_t o = 0;
+        for (size_t k = 0; k < prog.size(); ++k) {
+            while (o + 1 < out.size() && out[o].last <= prog[k].first) ++o;
+            remap[k] = (int64_t)o;
+        }
+        for (Step &st : out)
+            if (st.so_from >= 0) st.so_from = remap[st.so_from];
+    }
+    prog = std::move(out);
 }
 
 // A fused streaming kernel (mx_pw_..._f or _f_lo) specialised for the
@@ -2707,6 +3059,7 @@ int mxh_plan_program(const mx_plan_desc *plan, int repack, uint64_t *fused_ops, 
         mxh::Program pg;
         const bool rp = repack && plan->alias_parent && plan->alias_delta;
         pg.plan_fusion(plan, !rp);
+        if (rp && !std::getenv("MAXIM_NO_PAIR")) pg.plan_regions(plan);
         pg.layout(plan, rp);
         if (fused_ops) *fused_ops = pg.fused_ops;
         if (arena_len) *arena_len = pg.arena_len;
@@ -2724,6 +3077,7 @@ int mxh_plan_storage(const mx_plan_desc *plan, int repack, int64_t *owner) {
         mxh::Program pg;
         const bool rp = repack && plan->alias_parent && plan->alias_delta;
         pg.plan_fusion(plan, !rp);
+        if (rp && !std::getenv("MAXIM_NO_PAIR")) pg.plan_regions(plan);
         pg.layout(plan, rp);
         if (owner) memcpy(owner, pg.dbase.data(), sizeof(int64_t) * pg.dbase.size());
     });
@@ -2820,6 +3174,25 @@ int mxh_launch_info(mxh_gpu *g, uint64_t i, uint64_t *step, const char **kernel)
         if (i >= seq.size()) throw mx::Error("launch index out of range");
         if (step) *step = seq[i].first;
         if (kernel) *kernel = seq[i].second->name;
+    });
+}
+
+int mxh_launch_span(mxh_gpu *g, uint64_t i, uint64_t *ops) {
+    return guard([&] {
+        Gpu &x = *G(g);
+        const auto seq = x.launch_list();
+        if (i >= seq.size()) throw mx::Error("launch index out of range");
+        const mxh::Launch &l = *seq[i].second;
+        uint64_t first = seq[i].first, last = seq[i].first + 1;
+        if (x.fusion) {
+            first = x.prog[seq[i].first].first;
+            last = x.prog[seq[i].first].last;
+        }
+        const bool own = l.span[1] > l.span[0];
+        ops[0] = own ? l.span[0] : first;
+        ops[1] = own ? l.span[1] : last;
+        ops[2] = l.span[2];
+        ops[3] = l.span[3];
     });
 }
 

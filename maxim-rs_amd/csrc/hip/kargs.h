@@ -210,6 +210,13 @@ struct GemmArgs {
     LnOut lo;
 };
 
+// Two independent streaming-GEMM launches of one kernel in one grid: blocks
+// [0, na) run a, blocks [na, grid) run b (each with one batch).
+struct DualGemmArgs {
+    GemmArgs a, b;
+    uint32_t na, pad[3];
+};
+
 // Small GEMV for the plane-1 CALayer convs: y[o] = b[o] + sum_i w[o][i] x[i].
 struct GemvArgs {
     const float *w;

@@ -71,9 +71,11 @@ enum { EP_U = 1, EP_R1 = 2, EP_R2 = 4, EP_GELU = 8, EP_LRELU = 16, EP_YMAP = 32,
 // LN: 0 no folded LayerNorm; 1 the LayerNorm's expression on X,
 // (x - m) r w + c with w and c per input channel, in the LayerNorm kernels'
 // order (folding w and c into the weights changes the rounding).
+// (ux, nx): this block's index and the block count along x, by: the batch;
+// a kernel pairing two launches in one grid passes each part its own.
 template <int LAYOUT, int TMW, int KS, bool FUSED, int LN, bool XM = false, bool XMUL = false, bool CT = false,
           bool LNO = false, int EP = -1>
-__device__ void body(const GemmArgs &a) {
+__device__ void body(const GemmArgs &a, int ux, int nx, int by) {
     const bool has_u = EP < 0 ? a.e.u != nullptr : (EP & EP_U) != 0;
     const bool has_r1 = EP < 0 ? a.e.r1 != nullptr : (EP & EP_R1) != 0;
     const bool has_r2 = EP < 0 ? a.e.r2 != nullptr : (EP & EP_R2) != 0;
@@ -92,7 +94,7 @@ __device__ void body(const GemmArgs &a) {
     const int slen = LAYOUT == CH ? N : M;
     const int nib = (wout + TW - 1) / TW;
     const int ntiles = nib * ((slen + 63) / 64);  // < 2^31, checked by the host
-    const int b = blockIdx.y;
+    const int b = by;
     const float *W = a.A + (int64_t)b * a.sA;
     const float *X = a.B + (int64_t)b * a.sB;
     float *Y = a.C + (int64_t)b * a.sC;
@@ -104,8 +106,8 @@ __device__ void body(const GemmArgs &a) {
 
     // One XCD per contiguous range of blocks, so neighbouring tiles (which
     // share operands) meet in the same L2.
-    int unit = blockIdx.x;
-    const int nb = gridDim.x;
+    int unit = ux;
+    const int nb = nx;
     if ((nb & 7) == 0) unit = (unit & 7) * (nb >> 3) + (unit >> 3);
     const int tile = KS == 1 ? unit * 4 + wave : unit;
     if (tile >= ntiles) return;  // KS = 4: the whole block
@@ -523,10 +525,10 @@ __device__ void body(const GemmArgs &a) {
 // GemmArgs co / wd, wd % 4 == 0).
 #define MXK_PW2(LNAME, LAYOUT, TMW, KS, LN, XM, XMUL, SUF)                                         \
     extern "C" __global__ __launch_bounds__(256) void mx_pw_##LNAME##TMW##SUF(GemmArgs a) {        \
-        pw::body<pw::LAYOUT, TMW, KS, false, LN, XM, XMUL>(a);                                     \
+        pw::body<pw::LAYOUT, TMW, KS, false, LN, XM, XMUL>(a, blockIdx.x, gridDim.x, blockIdx.y);                                     \
     }                                                                                               \
     extern "C" __global__ __launch_bounds__(256) void mx_pw_##LNAME##TMW##SUF##_f(GemmArgs a) {    \
-        pw::body<pw::LAYOUT, TMW, KS, true, LN, XM, XMUL>(a);                                      \
+        pw::body<pw::LAYOUT, TMW, KS, true, LN, XM, XMUL>(a, blockIdx.x, gridDim.x, blockIdx.y);                                      \
     }
 #define MXK_PW1(LNAME, LAYOUT, TMW, KS, LN, XM, SUF) MXK_PW2(LNAME, LAYOUT, TMW, KS, LN, XM, false, SUF)
 #define MXK_PW(LNAME, LAYOUT, TMW)                                                                 \
@@ -535,13 +537,13 @@ __device__ void body(const GemmArgs &a) {
 #define MXK_PW_LN(TMW) MXK_PW1(ch, CH, TMW, 1, 1, false, _ln) MXK_PW1(ch, CH, TMW, 4, 1, false, _k4_ln)
 #define MXK_PW_CT(TMW, KS, SUF)                                                                    \
     extern "C" __global__ __launch_bounds__(256) void mx_pw_ch##TMW##SUF##_t(GemmArgs a) {          \
-        pw::body<pw::CH, TMW, KS, false, false, false, false, true>(a);                             \
+        pw::body<pw::CH, TMW, KS, false, false, false, false, true>(a, blockIdx.x, gridDim.x, blockIdx.y);                             \
     }
 // mx_pw_ch<TMW>[_k4][_ln]_f_lo: with a LayerNorm of one wave-wide band of
 // the output rows (GemmArgs lo).
 #define MXK_PW_LO(TMW, KS, LN, SUF)                                                               \
     extern "C" __global__ __launch_bounds__(256) void mx_pw_ch##TMW##SUF##_f_lo(GemmArgs a) {      \
-        pw::body<pw::CH, TMW, KS, true, LN, false, false, false, true>(a);                          \
+        pw::body<pw::CH, TMW, KS, true, LN, false, false, false, true>(a, blockIdx.x, gridDim.x, blockIdx.y);                          \
     }
 #define MXK_PW_MUL(TMW) \
     MXK_PW2(ch, CH, TMW, 1, false, false, true, _mul) MXK_PW2(ch, CH, TMW, 4, false, false, true, _k4_mul)
@@ -578,7 +580,19 @@ MXK_PW_LO(4, 4, 1, _k4_ln)
 // _f kernel otherwise (the same arithmetic in the same order).
 #define MXK_PW_E(NAME, LAYOUT, TMW, KS, LN, XM, XMUL, LNO, EP)                                     \
     extern "C" __global__ __launch_bounds__(256) void NAME##_e##EP(GemmArgs a) {                  \
-        pw::body<pw::LAYOUT, TMW, KS, true, LN, XM, XMUL, false, LNO, EP>(a);                      \
+        pw::body<pw::LAYOUT, TMW, KS, true, LN, XM, XMUL, false, LNO, EP>(a, blockIdx.x, gridDim.x, blockIdx.y); \
+    }
+// NAME_e<EP>_x2: two independent launches of that kernel as one grid (the
+// first d.na blocks run d.a, the rest d.b; one batch each), so that two
+// steps too small to fill the chip share its CUs and one launch's tail. Both
+// parts run the same function, so they share its LDS.
+#define MXK_PW_X2(NAME, LAYOUT, TMW, KS, LN, XM, XMUL, LNO, EP)                                    \
+    extern "C" __global__ __launch_bounds__(256) void NAME##_e##EP##_x2(DualGemmArgs d) {         \
+        if (blockIdx.x < d.na)                                                                     \
+            pw::body<pw::LAYOUT, TMW, KS, true, LN, XM, XMUL, false, LNO, EP>(d.a, blockIdx.x, d.na, 0); \
+        else                                                                                       \
+            pw::body<pw::LAYOUT, TMW, KS, true, LN, XM, XMUL, false, LNO, EP>(d.b, blockIdx.x - d.na, \
+                                                                            gridDim.x - d.na, 0);  \
     }
 MXK_PW_E(mx_pw_ch2_ln_f_lo, CH, 2, 1, 1, false, false, true, 72)
 MXK_PW_E(mx_pw_ch4_k4_ln_f_lo, CH, 4, 4, 1, false, false, true, 72)
@@ -605,3 +619,7 @@ MXK_PW_E(mx_pw_ch2_k4_mul_f, CH, 2, 4, 0, false, true, false, 66)
 MXK_PW_E(mx_pw_ch2_k4_mul_f, CH, 2, 4, 0, false, true, false, 70)
 MXK_PW_E(mx_pw_rw2_k4_f, RW, 2, 4, 0, false, false, false, 65)
 MXK_PW_E(mx_pw_rw4_k4_f, RW, 4, 4, 0, false, false, false, 65)
+MXK_PW_X2(mx_pw_ch2_ln_f_lo, CH, 2, 1, 1, false, false, true, 72)
+MXK_PW_X2(mx_pw_ch1_f, CH, 1, 1, 0, false, false, false, 226)
+MXK_PW_X2(mx_pw_ch2_f, CH, 2, 1, 0, false, false, false, 226)
+MXK_PW_X2(mx_pw_ch2_k4_f, CH, 2, 4, 0, false, false, false, 226)

@@ -52,6 +52,7 @@ def _lib():
             "mxh_time_ops": (I, [V, D, U, U, I, C.POINTER(C.c_float)]),
             "mxh_launches": (U, [V]),
             "mxh_launch_info": (I, [V, U, C.POINTER(C.c_uint64), C.POINTER(C.c_char_p)]),
+            "mxh_launch_span": (I, [V, U, C.POINTER(U)]),
             "mxh_launch_timeline": (I, [V, V, U]),
             "mxh_device_name": (C.c_char_p, [V]),
             "mxh_arena_bytes": (U, [V]),
@@ -224,6 +225,17 @@ class Gpu:
         for i in range(L.mxh_launches(self._h)):
             _check(L.mxh_launch_info(self._h, i, C.byref(st), C.byref(k)))
             out.append((st.value, k.value.decode()))
+        return out
+
+    def launch_spans(self):
+        """[((first, last), (first2, last2) or None)] - the ops each launch
+        computes (a second range for a launch pairing two steps' work)."""
+        L = _lib()
+        out = []
+        o = (C.c_uint64 * 4)()
+        for i in range(L.mxh_launches(self._h)):
+            _check(L.mxh_launch_span(self._h, i, o))
+            out.append(((o[0], o[1]), (o[2], o[3]) if o[3] > o[2] else None))
         return out
 
     def launch_timeline(self):

@@ -104,15 +104,16 @@ def test_timeline_and_counters(gpu_ok):
     assert per.shape == (1840,) and total > 0 and abs(per.sum() - total) < 1e-3 * total + 1e-3
     assert gpu.ops_launched == 1840
     assert gpu.kernels_launched >= 1840
-    assert gpu.arena_bytes <= 1.25 * plan.arena_bytes
+    assert gpu.arena_bytes <= 1.6 * plan.arena_bytes
     gpu.set_fusion(True)
     steps = gpu.steps()
     assert steps[0][0] == 0 and steps[-1][1] == 1840
     assert all(a[1] == b[0] for a, b in zip(steps, steps[1:]))
     # fused_ops counts the ops that launch nothing of their own: those folded
-    # into another op's step, and elided copies (a step with no kernel)
+    # into another op's step, and elided copies (a step with no kernel); a
+    # step that pairs two branches' launches stands for several such steps
     empty = sum(1 for _, _, k in steps if not k)
-    assert len(steps) - empty == 1840 - gpu.fused_ops
+    assert len(steps) - empty <= 1840 - gpu.fused_ops
     gpu.run(smooth_image(64, 64))
     per, total = gpu.timeline()
     assert per.shape == (len(steps),)
@@ -193,3 +194,43 @@ def test_runs_of_ops_that_cut_fused_steps(gpu_ok):
         gpu.run_ops(a, b)
     got = gpu.read_buf(plan.output).reshape(full.shape)
     assert np.array_equal(got.view(np.uint32), full.view(np.uint32))
+
+
+def test_gmlp_branches_share_launches(gpu_ok):
+    """At C4 the grid and block branches of the multi-axis gMLP blocks below
+    full resolution run their in- and out-projections as paired launches
+    (one grid for both): each paired launch names two disjoint op ranges
+    inside its step, with the same op sequence, and the pass still equals
+    the unpaired one to the bit (the paired steps' ops run in another order
+    only where nothing they touch overlaps)."""
+    import os
+    from maxim_amd import plan as P
+    from maxim_amd import hip as H
+    plan = P.Plan(weights("S-3"), 448, 640)
+    img = smooth_image(448, 640, seed=21)
+    gpu = H.Gpu(plan)
+    got = gpu.run(img).copy()
+    steps = gpu.steps()
+    pairs = 0
+    for (st, k), (r0, r1) in zip(gpu.launches(), gpu.launch_spans()):
+        a, b, _ = steps[st]
+        assert a <= r0[0] < r0[1] <= b
+        if r1 is None:
+            assert not k.endswith("_x2"), k
+            continue
+        pairs += 1
+        assert k.endswith("_x2") and a <= r1[0] < r1[1] <= b and (r0[1] <= r1[0] or r1[1] <= r0[0])
+        kinds = lambda r: [(op.kind, op.c_in, op.c_out, op.h * op.wd) for op in plan.ops[r[0]:r[1]]]
+        assert kinds(r0) == kinds(r1)
+    gpu.close()
+    print("%d paired launches" % pairs)
+    assert pairs >= 40
+    os.environ["MAXIM_NO_PAIR"] = "1"
+    try:
+        gpu = H.Gpu(plan)
+        assert not any(k.endswith("_x2") for _, k in gpu.launches())
+        ref = gpu.run(img)
+        gpu.close()
+    finally:
+        del os.environ["MAXIM_NO_PAIR"]
+    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))

@@ -57,7 +57,9 @@ def test_device_layout_is_sound(variant, h, w):
     print("%s %dx%d: %d of %d ops fused away, device arena %.1f MiB (plan %.1f MiB)"
           % (variant, h, w, fused, len(plan.ops), alen * 4 / 2**20, plan.arena_bytes / 2**20))
     assert fused >= 0.2 * len(plan.ops)
-    assert alen <= 1.25 * plan.arena_len
+    # the device layout packs by fused steps, but keeps the buffers of the
+    # paired gMLP branches apart over their regions (both run side by side)
+    assert alen <= 1.6 * plan.arena_len
     assert steps[0][0] == 0 and steps[-1][1] == len(plan.ops)
     base = base_of(plan)
 
