@@ -397,7 +397,7 @@ struct StepSpec {
     int64_t ln = -1;  // a LayerNorm op folded into the next op's GEMM (== first)
     bool epi = false;  // the producer applies readers in its epilogue
     int64_t perm = -1, pout = -1;  // a BlockPerm folded into the stores, and its source
-    int64_t out = -1, u = -1, r1 = -1, r2 = -1;
+    int64_t out = -1, u = -1, r1 = -1, r2 = -1, m = -1;
     int act = MXK_ACT_NONE;
     float slope = 0.0f;
     // An elided forward BlockPerm (op xperm / rperm, RULE_PERM_IN): the folded
@@ -1551,6 +1551,45 @@ void Program::plan_fusion(const mx_plan_desc *p, bool require_clear) {
             f.slope = n1.slope;
             f.out = n1.dst;
             f.last = g + 2;
+        } else if (o.kind == MX_OP_CONV3X3 && n1.kind == MX_OP_SIGMOID && n1.src == x && whole(n1, x)) {
+            // the supervised attention module's gate: sigmoid(conv) [* f] [+ r]
+            f.act = MXK_ACT_SIGMOID;
+            f.out = n1.dst;
+            f.last = g + 2;
+            if (g + 2 < p->n_ops) {
+                const mx_op &n2 = p->ops[g + 2];
+                const int64_t y = f.out;
+                if (n2.kind == MX_OP_MUL && (n2.src == y) != (n2.src2 == y) && whole(n2, y) &&
+                    only_reader(y, g + 1, g + 2)) {
+                    const int64_t mf = n2.src == y ? n2.src2 : n2.src;
+                    std::vector<int64_t> rr = reads;
+                    rr.insert(rr.end(), {mf, y});
+                    if (clear_of(n2.dst, rr)) {
+                        f.m = mf;
+                        f.out = n2.dst;
+                        f.last = g + 3;
+                        if (g + 3 < p->n_ops) {
+                            const mx_op &n3 = p->ops[g + 3];
+                            const int64_t z = f.out;
+                            if (n3.kind == MX_OP_ADD && (n3.src == z) != (n3.src2 == z) && whole(n3, z) &&
+                                only_reader(z, g + 2, g + 3)) {
+                                const int64_t r1 = n3.src == z ? n3.src2 : n3.src;
+                                rr.insert(rr.end(), {r1, z});
+                                if (clear_of(n3.dst, rr)) {
+                                    f.r1 = r1;
+                                    f.out = n3.dst;
+                                    f.last = g + 4;
+                                }
+                            }
+                        }
+                    }
+                }
+            }
+        } else if (o.kind == MX_OP_CONV3X3 && n1.kind == MX_OP_ADD && (n1.src == x) != (n1.src2 == x) &&
+                   whole(n1, x)) {
+            f.r1 = n1.src == x ? n1.src2 : n1.src;
+            f.out = n1.dst;
+            f.last = g + 2;
         } else if (o.kind == MX_OP_CONV1X1 && n1.kind == MX_OP_COPY && n1.src == x && whole(n1, x)) {
             f.out = n1.dst;
             f.last = g + 2;
@@ -1576,7 +1615,7 @@ void Program::plan_fusion(const mx_plan_desc *p, bool require_clear) {
             }
         }
         if (f.out >= 0) {
-            for (int64_t r : {f.u, f.r1, f.r2})
+            for (int64_t r : {f.u, f.r1, f.r2, f.m})
                 if (r >= 0) reads.push_back(r);
             f.epi = true;
             if (clear_of(f.out, reads)) sp = f;
@@ -1598,7 +1637,7 @@ void Program::plan_fusion(const mx_plan_desc *p, bool require_clear) {
         std::vector<int64_t> reads = reads_of(o);
         if (sp.ln >= 0) reads.push_back(p->ops[sp.ln].src);
         if (sp.xmul >= 0) for (int64_t r : reads_of(p->ops[sp.xmul])) reads.push_back(r);
-        for (int64_t r : {sp.u, sp.r1, sp.r2})
+        for (int64_t r : {sp.u, sp.r1, sp.r2, sp.m})
             if (r >= 0) reads.push_back(r);
         if (!clear_of(q.dst, reads)) return;
         sp.pout = x;
@@ -2262,11 +2301,12 @@ void Gpu::build_program(const mx_plan_desc *p) {
         e.u = dev(sp.u);
         e.r1 = dev(sp.r1);
         e.r2 = dev(sp.r2);
+        e.m = dev(sp.m);
         e.act = sp.act;
         e.slope = sp.slope;
         // 128-bit stores need every array the epilogue indexes like the
         // output on a 16-byte boundary.
-        const bool ealign = aligned(e.u, 16) && aligned(e.r1, 16) && aligned(e.r2, 16);
+        const bool ealign = aligned(e.u, 16) && aligned(e.r1, 16) && aligned(e.r2, 16) && aligned(e.m, 16);
         Launch l = base;
         if (!strncmp(l.name, "mx_pw_", 6) && !(ealign && aligned(dev(out), 16)))
             l = alt[g][0];  // the streaming kernels store 128 bits at a time
@@ -2772,8 +2812,10 @@ void Gpu::pair_launches(const mx_plan_desc *p) {
             return l.g[1] == 1 && l.g[2] == 1 && l.g[0] <= (unsigned)(5 * cus);
         };
         auto can_pair = [&](size_t u, size_t v) {
-            return kname(u) == kname(v) && one(u) && one(v) && !(reach[v] >> u & 1) && !(reach[u] >> v & 1) &&
-                   x2fn(kname(u)) != nullptr;
+            const bool ok = kname(u) == kname(v) && one(u) && one(v) && !(reach[v] >> u & 1) && !(reach[u] >> v & 1);
+            if (ok && !x2fn(kname(u)) && std::getenv("MAXIM_PAIR_LOG"))
+                fprintf(stderr, "maxim: no paired form of %s\n", kname(u));
+            return ok && x2fn(kname(u)) != nullptr;
         };
         // list scheduling: entries are (u) or (u, v)
         std::vector<std::pair<int, int>> seq;

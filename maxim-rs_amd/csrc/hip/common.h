@@ -59,12 +59,43 @@ __device__ __forceinline__ float gelu(float x) {
     return __builtin_fmaf(-ax, r, fmaxf(x, 0.0f));
 }
 
+// 1 / (1 + e^-x), the expression of the CPU path's sigmoid (one function, so
+// the standalone kernel, the CALayer block and the fused epilogue agree).
+__device__ __forceinline__ float sigmoid(float x) { return 1.0f / (1.0f + expf(-x)); }
+
 // The fused epilogue (kargs.h, Epilogue) for output element `idx`, after bias.
 __device__ __forceinline__ float epilogue(const Epilogue &e, float v, int64_t idx) {
     if (e.u) v = e.u[idx] * (v + 1.0f);
     if (e.act == MXK_ACT_GELU) v = gelu(v);
     else if (e.act == MXK_ACT_LRELU) v = v >= 0.0f ? v : e.slope * v;
+    else if (e.act == MXK_ACT_SIGMOID) v = sigmoid(v);
+    if (e.m) v = v * e.m[idx];
     if (e.r1) v = v + e.r1[idx];
     if (e.r2) v = v + e.r2[idx];
     return v;
+}
+
+// The same for the four elements idx .. idx + 3, with 128-bit operand loads
+// (idx % 4 == 0 and every operand 16-byte aligned): each element's operations
+// and their order are epilogue()'s.
+__device__ __forceinline__ void epilogue4(const Epilogue &e, float *v, int64_t idx) {
+    const float4 zero = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    const float4 u4 = e.u ? *reinterpret_cast<const float4 *>(e.u + idx) : zero;
+    const float4 m4 = e.m ? *reinterpret_cast<const float4 *>(e.m + idx) : zero;
+    const float4 a4 = e.r1 ? *reinterpret_cast<const float4 *>(e.r1 + idx) : zero;
+    const float4 b4 = e.r2 ? *reinterpret_cast<const float4 *>(e.r2 + idx) : zero;
+    const float uu[4] = {u4.x, u4.y, u4.z, u4.w}, mm[4] = {m4.x, m4.y, m4.z, m4.w};
+    const float aa[4] = {a4.x, a4.y, a4.z, a4.w}, bb[4] = {b4.x, b4.y, b4.z, b4.w};
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        float x = v[k];
+        if (e.u) x = uu[k] * (x + 1.0f);
+        if (e.act == MXK_ACT_GELU) x = gelu(x);
+        else if (e.act == MXK_ACT_LRELU) x = x >= 0.0f ? x : e.slope * x;
+        else if (e.act == MXK_ACT_SIGMOID) x = sigmoid(x);
+        if (e.m) x = x * mm[k];
+        if (e.r1) x = x + aa[k];
+        if (e.r2) x = x + bb[k];
+        v[k] = x;
+    }
 }

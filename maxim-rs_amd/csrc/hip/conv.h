@@ -210,9 +210,18 @@ __device__ void body(const ConvArgs &a) {
             float v[4] = {t.x, t.y, t.z, t.w};
             const int64_t idx = m * oplane + (int64_t)oy * a.ow + ox;
 #pragma unroll
-            for (int u = 0; u < 4; ++u) {
+            for (int u = 0; u < 4; ++u)
                 if (a.bias) v[u] = a.bias[m] + v[u];
-                if (FUSED) v[u] = epilogue(a.e, v[u], idx + u);
+            if (FUSED) {
+                // (past the row's end there is nothing to read: the lanes
+                // of a ragged last column group skip those elements)
+                if (a.cvec && ox + 3 < a.ow) {
+                    epilogue4(a.e, v, idx);
+                } else {
+#pragma unroll
+                    for (int u = 0; u < 4; ++u)
+                        if (ox + u < a.ow) v[u] = epilogue(a.e, v[u], idx + u);
+                }
             }
             if (a.cvec && ox + 3 < a.ow) {
                 st4(a.y + idx, make_float4(v[0], v[1], v[2], v[3]));

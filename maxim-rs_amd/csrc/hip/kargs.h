@@ -136,14 +136,17 @@ enum { MXK_EPI_PLAIN = 0, MXK_EPI_CONVT = 1 };
 
 // A fused epilogue, applied per output element after the bias and in the
 // order of the ops it replaces, so the result is the unfused kernels' to the
-// bit: v = bias + acc; [gate] v = u * (v + 1); [act] v = gelu(v) or lrelu(v);
-// [res1] v = v + r1; [res2] v = v + r2. u, r1, r2 are indexed like C.
-enum { MXK_ACT_NONE = 0, MXK_ACT_GELU = 1, MXK_ACT_LRELU = 2 };
+// bit: v = bias + acc; [gate] v = u * (v + 1); [act] v = gelu(v), lrelu(v)
+// or sigmoid(v); [mul] v = v * m; [res1] v = v + r1; [res2] v = v + r2.
+// u, m, r1, r2 are indexed like C. (The streaming GEMM kernels take gate,
+// GELU and the residuals; the convolutions every field.)
+enum { MXK_ACT_NONE = 0, MXK_ACT_GELU = 1, MXK_ACT_LRELU = 2, MXK_ACT_SIGMOID = 3 };
 
 struct Epilogue {
     const float *u;
     const float *r1;
     const float *r2;
+    const float *m;
     int32_t act;
     float slope;
 };

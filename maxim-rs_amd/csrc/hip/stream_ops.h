@@ -22,7 +22,7 @@ __device__ __forceinline__ float ew1(float a, float b, float slope) {
     if (OP == MXK_GATE_APPLY) return a * (b + 1.0f);
     if (OP == MXK_GELU) return gelu(a);
     if (OP == MXK_LRELU) return a >= 0.0f ? a : slope * a;
-    return 1.0f / (1.0f + expf(-a));  // MXK_SIGMOID
+    return sigmoid(a);  // MXK_SIGMOID
 }
 
 // Each thread moves UNROLL float4s spaced one block apart, so every load of a
@@ -168,7 +168,7 @@ __device__ __forceinline__ void ca_mlp_body(const CaArgs &a, const float *x) {
         float acc = a.b2 ? a.b2[o] : 0.0f;
 #pragma unroll 16
         for (int j = 0; j < a.r; ++j) acc += w[j] * h[j];
-        a.y[o] = 1.0f / (1.0f + expf(-acc));
+        a.y[o] = sigmoid(acc);
     }
 }
 

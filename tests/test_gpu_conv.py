@@ -81,3 +81,66 @@ def test_conv3x3_lrelu_fused(gpu_ok, misalign):
     assert len(steps) == 1 and steps[0][2].endswith("_f")
     assert steps[0][2].startswith("mx_wino3_")
     check(got, oracle_plan(cp, {0: x}, 3), "conv3x3 + lrelu, output misaligned %d" % misalign)
+
+
+def unfused(cp, inputs, out):
+    from maxim_amd import hip as H
+    gpu = H.Gpu(cp)
+    gpu.set_fusion(False)
+    for b, v in inputs.items():
+        gpu.write_buf(b, v)
+    gpu.run_ops(0, len(cp.ops))
+    got = gpu.read_buf(out).reshape(cp.bufs[out])
+    gpu.close()
+    return got
+
+
+@pytest.mark.parametrize("co,h,w", [(32, 12, 32), (64, 9, 21), (128, 8, 20)])
+def test_attention_gate_fused(gpu_ok, co, h, w):
+    """The supervised attention module's gate, Conv3x3 (3 -> co) -> Sigmoid
+    -> Mul -> Add, as one step whose conv epilogue applies all three (128-bit
+    operand reads where the rows allow, element by element at a ragged
+    edge): the unfused ops' bits, and the CPU path within the GEMM bar."""
+    from maxim_amd import plan as P
+    rng = np.random.default_rng(co + w)
+    img = rng.standard_normal((3, h, w)).astype(np.float32)
+    f1 = rng.standard_normal((co, h, w)).astype(np.float32)
+    res = rng.standard_normal((co, h, w)).astype(np.float32)
+    wt = he(rng, (co, 3, 3, 3), 27)
+    b = (rng.standard_normal(co) * 0.1).astype(np.float32)
+    n = co * h * w
+    bufs = [(3, h, w), (co, h, w), (co, h, w), (co, h, w), (co, h, w), (co, h, w), (co, h, w)]
+    ops = [P.make_op(P.CONV3X3, dst=1, src=0, w=0, bias=1, c_in=3, c_out=co, h=h, wd=w),
+           P.make_op(P.SIGMOID, dst=2, src=1, n=n),
+           P.make_op(P.MUL, dst=4, src=2, src2=3, n=n),
+           P.make_op(P.ADD, dst=6, src=4, src2=5, n=n)]
+    cp = P.CustomPlan(bufs, ops, [wt, b], input=0, output=6)
+    inputs = {0: img, 3: f1, 5: res}
+    got, steps = run_plan(cp, inputs, 6)
+    print("steps", steps)
+    assert len(steps) == 1 and steps[0][2].endswith("_f"), steps
+    assert np.array_equal(got.view(np.uint32), unfused(cp, inputs, 6).view(np.uint32))
+    check(got, oracle_plan(cp, inputs, 6), "conv3x3 3->%d + sigmoid * f + r @%dx%d" % (co, h, w))
+
+
+@pytest.mark.parametrize("ci,h,w", [(64, 10, 64), (32, 13, 21)])
+def test_conv3x3_add_fused(gpu_ok, ci, h, w):
+    """A stage's output image: Conv3x3 (ci -> 3) -> Add (the input image) as
+    one step with the add in the conv's epilogue; the unfused bits, and the
+    CPU path within the GEMM bar."""
+    from maxim_amd import plan as P
+    rng = np.random.default_rng(ci + w)
+    x = rng.standard_normal((ci, h, w)).astype(np.float32)
+    img = rng.standard_normal((3, h, w)).astype(np.float32)
+    wt = he(rng, (3, ci, 3, 3), 9 * ci)
+    b = (rng.standard_normal(3) * 0.1).astype(np.float32)
+    bufs = [(ci, h, w), (3, h, w), (3, h, w), (3, h, w)]
+    ops = [P.make_op(P.CONV3X3, dst=1, src=0, w=0, bias=1, c_in=ci, c_out=3, h=h, wd=w),
+           P.make_op(P.ADD, dst=3, src=1, src2=2, n=3 * h * w)]
+    cp = P.CustomPlan(bufs, ops, [wt, b], input=0, output=3)
+    inputs = {0: x, 2: img}
+    got, steps = run_plan(cp, inputs, 3)
+    print("steps", steps)
+    assert len(steps) == 1 and steps[0][2].endswith("_f"), steps
+    assert np.array_equal(got.view(np.uint32), unfused(cp, inputs, 3).view(np.uint32))
+    check(got, oracle_plan(cp, inputs, 3), "conv3x3 %d->3 + image @%dx%d" % (ci, h, w))
