@@ -383,6 +383,18 @@ def launch_costs(plan, steps, launches, R, spans=None):
         if len(idx) == 1:
             out[idx[0]] = step_cost(a, b)
             continue
+        if o.kind == P.RESIZE and b - a == 2 and plan.ops[a + 1].kind == P.CONV1X1 and len(idx) == 2:
+            # a commuted UpSampleRatio: the conv at the resize's input
+            # resolution, then the resize of the conv's c_out channels
+            c = plan.ops[a + 1]
+            pl, opl = o.h * o.wd, o.oh * o.ow
+            bias = c.c_out if c.bias >= 0 else 0
+            for i, kn in zip(idx, names):
+                if kn.startswith("mx_resize"):
+                    out[i] = (0, 4 * c.c_out * (pl + opl))
+                else:
+                    out[i] = (2 * c.c_in * c.c_out * pl, 4 * (c.c_in * pl + c.c_out * pl + c.c_in * c.c_out + bias))
+            continue
         for i, kn in zip(idx, names):
             if kn.startswith("mx_chan_ln_stats"):
                 out[i] = (0, 4 * (o.c * o.hw + 2 * o.hw))

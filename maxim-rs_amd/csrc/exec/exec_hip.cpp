@@ -389,7 +389,7 @@ std::string conv_name(ConvCfg c, bool k3) {
 
 // What the executor decides about a plan before touching the device: which
 // ops fuse into which steps, and where every buffer lives in the device arena.
-enum { RULE_NONE = 0, RULE_CA_MLP = 1, RULE_SCALE_ADD = 2, RULE_ELIDED = 3, RULE_PERM_IN = 4 };
+enum { RULE_NONE = 0, RULE_CA_MLP = 1, RULE_SCALE_ADD = 2, RULE_ELIDED = 3, RULE_PERM_IN = 4, RULE_RS_CONV = 5 };
 
 struct StepSpec {
     uint64_t first = 0, last = 0;
@@ -456,7 +456,7 @@ public:
     unsigned char *wdev = nullptr;
     uint64_t wbytes = 0;
     float *scratch = nullptr;
-    uint64_t scratch_len = 0, ln_off = 0, so_base = 0;
+    uint64_t scratch_len = 0, ln_off = 0, so_base = 0, rs_off = 0;
     uint64_t n_ops = 0, n_bufs = 0;
     std::vector<std::vector<Launch>> ops;
     uint64_t launched = 0, kernels = 0;
@@ -993,7 +993,16 @@ void Gpu::init(const mx_plan_desc *p) {
         if (sp.ln >= 0) ln_need = std::max<uint64_t>(ln_need, 2 * (uint64_t)p->ops[sp.ln].hw);
     // then the statistics that steps' epilogues leave for later steps
     so_base = (ln_off + ln_need + 63) & ~(uint64_t)63;
-    scratch_len = std::max<uint64_t>(so_base + pg.so_len, 64);
+    // then the low-resolution 1x1 conv outputs of commuted Resize -> Conv1x1
+    // steps (one step at a time)
+    uint64_t rs_need = 0;
+    for (const StepSpec &sp : pg.specs)
+        if (sp.rule == RULE_RS_CONV) {
+            const mx_op &r = p->ops[sp.first], &c = p->ops[sp.first + 1];
+            rs_need = std::max<uint64_t>(rs_need, (uint64_t)(c.c_out * r.h * r.wd));
+        }
+    rs_off = (so_base + pg.so_len + 63) & ~(uint64_t)63;
+    scratch_len = std::max<uint64_t>(rs_off + rs_need, 64);
     const uint64_t need = arena_len * 4 + wbytes + scratch_len * 4;
     size_t free_b = 0, total_b = 0;
     if (H.hipMemGetInfo(&free_b, &total_b) == 0 && need > free_b) {
@@ -1474,6 +1483,7 @@ void Program::plan_fusion(const mx_plan_desc *p, bool require_clear) {
         return R{p->offs[id], p->offs[id] + (uint64_t)(s.c * s.h * s.w)};
     };
     auto overlap = [](R x, R y) { return x.a < y.b && y.a < x.b; };
+    const bool commute = !std::getenv("MAXIM_NO_COMMUTE");
     // Whether buffer `id` must stay intact to the end of a pass (a named
     // dump): the plan marks the storage owner, so a view is kept when its
     // root (following alias_parent) is.
@@ -1765,6 +1775,23 @@ void Program::plan_fusion(const mx_plan_desc *p, bool require_clear) {
             sp.rule = RULE_CA_MLP;
             sp.out = p->ops[i + 3].dst;
             sp.last = i + 4;
+        }
+        // Upsampling Resize -> 1x1 conv to fewer channels (the reference's
+        // UpSampleRatio): the conv runs first, at the input resolution, and the
+        // resize then interpolates its c_out channels instead of the c_in
+        // channels it was given. Both are linear, the resize acts on each
+        // channel plane alone with taps that sum to 1, and the conv on each
+        // pixel alone, so W R(x) + b = R(W x + b) up to rounding; the pair
+        // moves and multiplies (c_out / c_in) x (input / output pixels) of the
+        // data. Not bit-preserving: MAXIM_NO_COMMUTE=1 keeps the plan's order.
+        if (sp.rule == RULE_NONE && commute && o.kind == MX_OP_RESIZE && i + 1 < p->n_ops) {
+            const mx_op &n1 = p->ops[i + 1];
+            if (n1.kind == MX_OP_CONV1X1 && n1.src == o.dst && n1.c_in == o.c && n1.c_out < o.c &&
+                n1.h == o.oh && n1.wd == o.ow && o.oh >= o.h && o.ow >= o.wd && o.oh * o.ow > o.h * o.wd &&
+                !kept(o.dst) && only_reader(o.dst, i, i + 1) && clear_of(n1.dst, {o.src})) {
+                sp.rule = RULE_RS_CONV;
+                sp.last = i + 2;
+            }
         }
         // ChanScale -> Add: y = x * s + r in one pass.
         if (sp.rule == RULE_NONE && o.kind == MX_OP_CHAN_SCALE && i + 1 < p->n_ops) {
@@ -2505,6 +2532,39 @@ void Gpu::build_program(const mx_plan_desc *p) {
     for (const StepSpec &sp : pg.specs) {
         if (sp.rule == RULE_ELIDED) {
             prog.push_back(Step{sp.first, sp.last, {}});
+            continue;
+        }
+        if (sp.rule == RULE_RS_CONV) {
+            // the conv's own GEMM over the resize's input plane into scratch,
+            // then the resize's own launch over the conv's c_out channels
+            // into the conv's output
+            const mx_op &r = p->ops[sp.first], &c = p->ops[sp.first + 1];
+            const std::vector<Launch> &rl = ops[sp.first], &cl = ops[sp.first + 1];
+            Step st{sp.first, sp.last, {}};
+            if (rl.size() == 1 && !strncmp(rl[0].name, "mx_resize_hv", 12) && cl.size() == 1 && cl[0].kind == 1 &&
+                (r.h * r.wd) % 4 == 0) {
+                GemmArgs a;
+                memcpy(&a, cl[0].a0, sizeof a);
+                float *out = a.C;
+                a.B = dev(r.src);
+                a.N = (int32_t)(r.h * r.wd);
+                a.C = scratch + rs_off;
+                Launch g;
+                if (a.batch == 1 && a.M == c.c_out && try_pw(0, a, g)) {
+                    Resize2Args z;
+                    memcpy(&z, rl[0].a0, sizeof z);
+                    z.x = scratch + rs_off;
+                    z.y = out;
+                    Launch zl = rl[0];
+                    zl.g[1] = (unsigned)c.c_out;
+                    set_args(zl, z);
+                    st.launches = {g, zl};
+                }
+            }
+            if (st.launches.empty())  // the plan's order, op by op
+                for (uint64_t k = sp.first; k < sp.last; ++k)
+                    for (const Launch &x : ops[k]) st.launches.push_back(x);
+            prog.push_back(st);
             continue;
         }
         if (sp.rule == RULE_PERM_IN) {
