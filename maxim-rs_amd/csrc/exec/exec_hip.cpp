@@ -86,7 +86,7 @@ struct Launch {
     unsigned g[3] = {1, 1, 1};
     unsigned b[3] = {MXK_BLOCK, 1, 1};
     unsigned shm = 0;  // dynamic LDS bytes
-    alignas(16) unsigned char a0[736];
+    alignas(16) unsigned char a0[768];
     alignas(16) unsigned char a1[32];
     int nparams = 1;
     int kind = 0;  // 1: a0 holds GemmArgs (plain epilogue), 2: ConvArgs, 3: DualGemmArgs
@@ -677,6 +677,8 @@ private:
     std::vector<std::vector<Launch>> alt;
     std::vector<char> whole_k;  // per op: keep a streaming GEMM's reduction in one wave
     bool no_pw = getenv("MAXIM_NO_PW") != nullptr;
+    // keep the plan's order of arithmetic everywhere (fused = unfused to the bit)
+    bool plan_order = getenv("MAXIM_PLAN_ORDER") != nullptr;
     void validate(const mx_plan_desc *p) const;
     void build_launches(const mx_plan_desc *p, const std::vector<int64_t> &woff,
                         const std::vector<std::array<int64_t, 4>> &extra,
@@ -1483,7 +1485,7 @@ void Program::plan_fusion(const mx_plan_desc *p, bool require_clear) {
         return R{p->offs[id], p->offs[id] + (uint64_t)(s.c * s.h * s.w)};
     };
     auto overlap = [](R x, R y) { return x.a < y.b && y.a < x.b; };
-    const bool commute = !std::getenv("MAXIM_NO_COMMUTE");
+    const bool commute = !std::getenv("MAXIM_PLAN_ORDER");
     // Whether buffer `id` must stay intact to the end of a pass (a named
     // dump): the plan marks the storage owner, so a view is kept when its
     // root (following alias_parent) is.
@@ -1783,7 +1785,7 @@ void Program::plan_fusion(const mx_plan_desc *p, bool require_clear) {
         // channel plane alone with taps that sum to 1, and the conv on each
         // pixel alone, so W R(x) + b = R(W x + b) up to rounding; the pair
         // moves and multiplies (c_out / c_in) x (input / output pixels) of the
-        // data. Not bit-preserving: MAXIM_NO_COMMUTE=1 keeps the plan's order.
+        // data. Not bit-preserving: MAXIM_PLAN_ORDER=1 keeps the plan's order.
         if (sp.rule == RULE_NONE && commute && o.kind == MX_OP_RESIZE && i + 1 < p->n_ops) {
             const mx_op &n1 = p->ops[i + 1];
             if (n1.kind == MX_OP_CONV1X1 && n1.src == o.dst && n1.c_in == o.c && n1.c_out < o.c &&
@@ -2703,12 +2705,18 @@ void Gpu::build_program(const mx_plan_desc *p) {
         set_args(sl, sa);
         const std::string gname = gl.name;
         const bool f = gname.size() > 2 && gname.compare(gname.size() - 2, 2, "_f") == 0;
-        gl.name = intern((f ? gname.substr(0, gname.size() - 2) : gname) + "_ln" + (f ? "_f" : ""));
-        gl.f = fn(gl.name);
+        // With no statistics from a producer, a split-reduction GEMM over a
+        // 128-channel LayerNorm (each of the block's waves holds 32 channels
+        // of every pixel it reads) forms them itself (_ln2): no statistics
+        // pass. Its sums run in another order than the LayerNorm kernels',
+        // so MAXIM_PLAN_ORDER=1 keeps the pass.
         GemmArgs a;
         memcpy(&a, gl.a0, sizeof a);
+        const bool ln2 = !so && !plan_order && gname.rfind("mx_pw_ch2_k4", 0) == 0 && a.K == 128 && ln.c == 128;
+        gl.name = intern((f ? gname.substr(0, gname.size() - 2) : gname) + (ln2 ? "_ln2" : "_ln") + (f ? "_f" : ""));
+        gl.f = fn(gl.name);
         a.B = la.x;
-        a.ln = LnIn{stats, stats + ln.hw, la.scale, la.bias};
+        a.ln = LnIn{ln2 ? nullptr : stats, ln2 ? nullptr : stats + ln.hw, la.scale, la.bias, la.eps, 0};
         if (xmap) {
             const mx_op &q = p->ops[sp.xperm];
             a.xmap = mx_block_map(q, 0);
@@ -2718,7 +2726,7 @@ void Gpu::build_program(const mx_plan_desc *p) {
         if (so) {
             st.so_from = sp.so_from;
             st.pre.push_back(sl);
-        } else {
+        } else if (!ln2) {
             st.launches.push_back(sl);
         }
         st.main = st.launches.size();

@@ -153,9 +153,13 @@ struct Epilogue {
 
 // A channel LayerNorm folded into a GEMM's X operand (channel-major layout):
 // X[k][n] is used as (X[k][n] - mean[n]) * rstd[n] * scale[k] + bias[k], the
-// LayerNorm kernels' own expression, with mean/rstd from mx_chan_ln_stats.
+// LayerNorm kernels' own expression, with mean/rstd from mx_chan_ln_stats
+// (or, in the split-reduction kernels' _ln2 form, from the X tile the block
+// holds: mean/rstd unused, eps the LayerNorm's).
 struct LnIn {
     const float *mean, *rstd, *scale, *bias;
+    float eps;  // mode 2 (the statistics computed by the GEMM itself)
+    int32_t pad;
 };
 
 // A block permutation folded into a GEMM (BlockPerm, no swap,

@@ -70,7 +70,13 @@ enum { EP_U = 1, EP_R1 = 2, EP_R2 = 4, EP_GELU = 8, EP_LRELU = 16, EP_YMAP = 32,
 
 // LN: 0 no folded LayerNorm; 1 the LayerNorm's expression on X,
 // (x - m) r w + c with w and c per input channel, in the LayerNorm kernels'
-// order (folding w and c into the weights changes the rounding).
+// order (folding w and c into the weights changes the rounding), with m and r
+// read from a statistics pass; 2 the same with m and r computed here, from
+// the X tile the block's four waves hold between them (KS = 4 with two
+// supersteps per wave: 128 channels), so no statistics pass runs. Mode 2
+// sums each pixel's channels in another order than the LayerNorm kernels
+// (a wave's 32 in its lanes' order, the four lane groups pairwise, then the
+// waves in turn), so its normalised X differs from theirs by rounding.
 // (ux, nx): this block's index and the block count along x, by: the batch;
 // a kernel pairing two launches in one grid passes each part its own.
 template <int LAYOUT, int TMW, int KS, bool FUSED, int LN, bool XM = false, bool XMUL = false, bool CT = false,
@@ -166,10 +172,12 @@ __device__ void body(const GemmArgs &a, int ux, int nx, int by) {
     // the whole tile, and each superstep's scale/bias for k = 16 S + 4 g + q.
     float4 lmean, lrstd;
     const float *lsc = nullptr, *lbi = nullptr;
-    if (LN) {  // a single 1x1 conv (no batch): statistics indexed like X's columns
+    if (LN == 1) {  // a single 1x1 conv (no batch): statistics indexed like X's columns
         lmean = ld4(a.ln.mean + xcol);
         lrstd = ld4(a.ln.rstd + xcol);
-        if (LN == 1) {
+    }
+    if (LN) {
+        {
             lsc = a.ln.scale + 4 * g + S0 * 16;
             lbi = a.ln.bias + 4 * g + S0 * 16;
         }
@@ -187,7 +195,7 @@ __device__ void body(const GemmArgs &a, int ux, int nx, int by) {
         }
 #pragma unroll
         for (int mt = 0; mt < TMW; ++mt) wv[mt] = ld4(wp[mt] + s * 16);
-        if (LN == 1) {
+        if (LN) {
             lv[0] = ld4(lsc + s * 16);
             lv[1] = ld4(lbi + s * 16);
         }
@@ -246,6 +254,68 @@ __device__ void body(const GemmArgs &a, int ux, int nx, int by) {
     // it), so the wait before each multiply counts only the loads it needs.
     load(0, xa, wa, la, ma);
     load(min(1, nSw - 1), xb, wb, lb, mb);
+    if constexpr (LN == 2) {
+        static_assert(KS == 4 && LAYOUT == CH, "in-kernel statistics: the split-reduction channel-major form");
+        // This lane's rows k = 16 S + 4 g + q of its two supersteps (xa, xb)
+        // for pixels xcol .. xcol + 3; lanes i, i + 16, i + 32 and i + 48
+        // hold the same pixels, the four waves the four quarters of k.
+        __shared__ float4 lst[4][16][2];
+        float4 p1 = xa[0], p2 = make_float4(xa[0].x * xa[0].x, xa[0].y * xa[0].y, xa[0].z * xa[0].z, xa[0].w * xa[0].w);
+        auto add = [&](const float4 &v) {
+            p1.x = p1.x + v.x;
+            p1.y = p1.y + v.y;
+            p1.z = p1.z + v.z;
+            p1.w = p1.w + v.w;
+            p2.x = p2.x + v.x * v.x;
+            p2.y = p2.y + v.y * v.y;
+            p2.z = p2.z + v.z * v.z;
+            p2.w = p2.w + v.w * v.w;
+        };
+#pragma unroll
+        for (int q = 1; q < 4; ++q) add(xa[q]);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) add(xb[q]);
+#pragma unroll
+        for (int d = 16; d <= 32; d *= 2) {
+            p1.x = p1.x + __shfl_xor(p1.x, d);
+            p1.y = p1.y + __shfl_xor(p1.y, d);
+            p1.z = p1.z + __shfl_xor(p1.z, d);
+            p1.w = p1.w + __shfl_xor(p1.w, d);
+            p2.x = p2.x + __shfl_xor(p2.x, d);
+            p2.y = p2.y + __shfl_xor(p2.y, d);
+            p2.z = p2.z + __shfl_xor(p2.z, d);
+            p2.w = p2.w + __shfl_xor(p2.w, d);
+        }
+        if (g == 0) {
+            lst[wave][i][0] = p1;
+            lst[wave][i][1] = p2;
+        }
+        __syncthreads();
+        float4 s1 = lst[0][i][0], s2 = lst[0][i][1];
+#pragma unroll
+        for (int w = 1; w < 4; ++w) {
+            const float4 t1 = lst[w][i][0], t2 = lst[w][i][1];
+            s1.x = s1.x + t1.x;
+            s1.y = s1.y + t1.y;
+            s1.z = s1.z + t1.z;
+            s1.w = s1.w + t1.w;
+            s2.x = s2.x + t2.x;
+            s2.y = s2.y + t2.y;
+            s2.z = s2.z + t2.z;
+            s2.w = s2.w + t2.w;
+        }
+        // mean, then 1 / std, as the LayerNorm statistics kernels form them
+        const float nf = (float)K;
+        auto stat = [&](float a1, float a2, float &m, float &r) {
+            m = a1 / nf;
+            const float var = a2 / nf - m * m;
+            r = 1.0f / sqrtf(fmaxf(var, 0.0f) + a.ln.eps);
+        };
+        stat(s1.x, s2.x, lmean.x, lrstd.x);
+        stat(s1.y, s2.y, lmean.y, lrstd.y);
+        stat(s1.z, s2.z, lmean.z, lrstd.z);
+        stat(s1.w, s2.w, lmean.w, lrstd.w);
+    }
     mma(xa, wa, la, ma, true);
     int s = 1;
     for (; s + 2 <= nSw; s += 2) {
@@ -535,6 +605,8 @@ __device__ void body(const GemmArgs &a, int ux, int nx, int by) {
     MXK_PW1(LNAME, LAYOUT, TMW, 1, false, false, ) MXK_PW1(LNAME, LAYOUT, TMW, 4, false, false, _k4) \
     MXK_PW1(LNAME, LAYOUT, TMW, 1, false, true, _xm) MXK_PW1(LNAME, LAYOUT, TMW, 4, false, true, _k4_xm)
 #define MXK_PW_LN(TMW) MXK_PW1(ch, CH, TMW, 1, 1, false, _ln) MXK_PW1(ch, CH, TMW, 4, 1, false, _k4_ln)
+// _k4_ln2: the LayerNorm statistics computed by the block itself (LN = 2)
+MXK_PW1(ch, CH, 2, 4, 2, false, _k4_ln2)
 #define MXK_PW_CT(TMW, KS, SUF)                                                                    \
     extern "C" __global__ __launch_bounds__(256) void mx_pw_ch##TMW##SUF##_t(GemmArgs a) {          \
         pw::body<pw::CH, TMW, KS, false, false, false, false, true>(a, blockIdx.x, gridDim.x, blockIdx.y);                             \
@@ -598,6 +670,7 @@ MXK_PW_E(mx_pw_ch2_ln_f_lo, CH, 2, 1, 1, false, false, true, 72)
 MXK_PW_E(mx_pw_ch4_k4_ln_f_lo, CH, 4, 4, 1, false, false, true, 72)
 MXK_PW_E(mx_pw_ch2_ln_f, CH, 2, 1, 1, false, false, false, 72)
 MXK_PW_E(mx_pw_ch2_k4_ln_f, CH, 2, 4, 1, false, false, false, 72)
+MXK_PW_E(mx_pw_ch2_k4_ln2_f, CH, 2, 4, 2, false, false, false, 72)
 MXK_PW_E(mx_pw_ch2_f_lo, CH, 2, 1, 0, false, false, true, 64)
 MXK_PW_E(mx_pw_ch2_f_lo, CH, 2, 1, 0, false, false, true, 66)
 MXK_PW_E(mx_pw_ch2_k4_f_lo, CH, 2, 4, 0, false, false, true, 64)

@@ -11,7 +11,7 @@ W R(x) + b = R(W x + b) up to rounding. The tests pin:
 - the commuted pair against the plan's own order on the device (rounding
   only: 4e-6 of the output's magnitude) and against the CPU path at the GEMM
   bar (1e-4 * max|cpu|);
-- MAXIM_NO_COMMUTE=1 restores the plan's order: fused = unfused to the bit.
+- MAXIM_PLAN_ORDER=1 restores the plan's order: fused = unfused to the bit.
 """
 
 import os
@@ -46,15 +46,15 @@ def pair_plan(ci, h, w, oh, ow, co, seed):
 
 def run(cp, x, fused, no_commute=False):
     from maxim_amd import hip as H
-    old = os.environ.pop("MAXIM_NO_COMMUTE", None)
+    old = os.environ.pop("MAXIM_PLAN_ORDER", None)
     if no_commute:
-        os.environ["MAXIM_NO_COMMUTE"] = "1"
+        os.environ["MAXIM_PLAN_ORDER"] = "1"
     try:
         gpu = H.Gpu(cp)
     finally:
-        os.environ.pop("MAXIM_NO_COMMUTE", None)
+        os.environ.pop("MAXIM_PLAN_ORDER", None)
         if old is not None:
-            os.environ["MAXIM_NO_COMMUTE"] = old
+            os.environ["MAXIM_PLAN_ORDER"] = old
     gpu.set_fusion(fused)
     gpu.write_buf(0, x)
     gpu.run_ops(0, len(cp.ops))

@@ -145,7 +145,7 @@ def test_fusion_is_bitwise_transparent(gpu_ok, variant, side, monkeypatch):
     gpu = H.Gpu(plan)
     c = gpu.run(img).copy()
     gpu.close()
-    monkeypatch.setenv("MAXIM_NO_COMMUTE", "1")
+    monkeypatch.setenv("MAXIM_PLAN_ORDER", "1")
     gpu = H.Gpu(plan)
     gpu.set_fusion(False)
     a = gpu.run(img).copy()
@@ -186,7 +186,7 @@ def test_runs_of_ops_that_cut_fused_steps(gpu_ok, monkeypatch):
     that commutes UpSampleRatio's resize and conv is off here)."""
     from maxim_amd import plan as P
     from maxim_amd import hip as H
-    monkeypatch.setenv("MAXIM_NO_COMMUTE", "1")
+    monkeypatch.setenv("MAXIM_PLAN_ORDER", "1")
     plan = P.Plan(weights("S-3"), 64, 64)
     img = smooth_image(64, 64, seed=13)
     gpu = H.Gpu(plan)
