@@ -1,4 +1,6 @@
-"""Upsampling Resize -> 1x1 conv (the reference's UpSampleRatio,
+"""The two rules that reorder arithmetic (MAXIM_PLAN_ORDER=1 turns both off).
+
+Upsampling Resize -> 1x1 conv (the reference's UpSampleRatio,
 src/model.rs builds it as a Resize op followed by a Conv1x1 op) run in the
 other order: the conv at the resize's input resolution, then the resize of
 the conv's fewer channels.
@@ -136,3 +138,61 @@ def test_cut_inside_commuted_pair(gpu_ok):
     got = gpu.read_buf(3).reshape(cp.bufs[3])
     gpu.close()
     assert np.array_equal(got.view(np.uint32), plain.view(np.uint32))
+
+
+@pytest.mark.parametrize("h,w", [(56, 80), (30, 44)])
+def test_split_gemm_layernorm_statistics(gpu_ok, h, w):
+    """ChanLn over 128 channels -> 1x1 conv with the split reduction: the
+    GEMM forms each pixel's statistics from the channels its block's four
+    waves hold (the _k4_ln2 kernels, no statistics pass). Against the CPU
+    path at the GEMM bar, inputs with a per-pixel offset of 3 and spread 0.5
+    (so the one-pass variance matters), plane sizes with and without a
+    ragged last tile; MAXIM_PLAN_ORDER=1 restores the statistics pass and
+    the unfused bits."""
+    from maxim_amd import plan as P
+    from oracle import oracle as O
+    rng = np.random.default_rng(h + w)
+    c, co = 128, 96
+    x = (3.0 + 0.5 * rng.standard_normal((c, h, w)) + rng.standard_normal((1, h, w))).astype(np.float32)
+    scale = rng.normal(1.0, 0.1, c).astype(np.float32)
+    shift = rng.normal(0.0, 0.1, c).astype(np.float32)
+    wt = (rng.standard_normal((co, c)) * np.sqrt(2.0 / c)).astype(np.float32)
+    b = rng.normal(0, 0.1, co).astype(np.float32)
+    ops = [P.make_op(P.CHAN_LN, dst=1, src=0, scale=0, bias=1, c=c, hw=h * w),
+           P.make_op(P.CONV1X1, dst=2, src=1, w=2, bias=3, c_in=c, c_out=co, h=h, wd=w)]
+    cp = P.CustomPlan([(c, h, w), (c, h, w), (co, h, w)], ops, [scale, shift, wt.ravel(), b], input=0, output=2)
+
+    def go(fused, plan_order=False):
+        from maxim_amd import hip as H
+        old = os.environ.pop("MAXIM_PLAN_ORDER", None)
+        if plan_order:
+            os.environ["MAXIM_PLAN_ORDER"] = "1"
+        try:
+            gpu = H.Gpu(cp)
+        finally:
+            os.environ.pop("MAXIM_PLAN_ORDER", None)
+            if old is not None:
+                os.environ["MAXIM_PLAN_ORDER"] = old
+        gpu.set_fusion(fused)
+        gpu.write_buf(0, x)
+        gpu.run_ops(0, 2)
+        out = gpu.read_buf(2).reshape(co, h, w)
+        ks = [k for _, k in gpu.launches()]
+        gpu.close()
+        return out, ks
+
+    got, ks = go(True)
+    print(ks)
+    assert any(k.startswith("mx_pw_ch2_k4_ln2") for k in ks) and not any(k.startswith("mx_chan_ln") for k in ks), ks
+    arena = np.zeros(cp.arena_len, np.float32)
+    arena[:x.size] = x.ravel()
+    O.run(cp, arena)
+    o = int(cp.offs[2])
+    ref = arena[o:o + co * h * w].reshape(co, h, w).astype(np.float64)
+    err = float(np.abs(got.astype(np.float64) - ref).max())
+    print("max|cpu| %.3g, max-abs %.3g" % (float(np.abs(ref).max()), err))
+    assert np.isfinite(got).all() and err <= 1e-4 * float(np.abs(ref).max())
+    kept, ks2 = go(True, plan_order=True)
+    plain, _ = go(False)
+    assert any(k.startswith("mx_chan_ln_stats") for k in ks2), ks2
+    assert np.array_equal(kept.view(np.uint32), plain.view(np.uint32))
