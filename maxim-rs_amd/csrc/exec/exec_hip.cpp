@@ -1389,8 +1389,13 @@ void Gpu::build_launches(const mx_plan_desc *p, const std::vector<int64_t> &woff
                     bool done = false;
                     for (int tw : {256, 64}) {
                         if (tw == 256 && (o.ow < o.wd || o.ow % 4 || !aligned(B(o.dst), 16))) continue;
-                        const int span = resize_band(th, mh, o.ow, tw);
+                        int span = resize_band(th, mh, o.ow, tw);
                         if (span < 0) continue;
+                        // rows staged with 128-bit loads from the 16-byte
+                        // boundary at or before a block's first column: up to
+                        // 6 more columns, rows a multiple of 4 apart in LDS
+                        const bool vec = o.wd % 4 == 0 && aligned(B(o.src), 16);
+                        if (vec) span = (span + 6 + 3) & ~3;
                         const int64_t tiles_x = cdiv(o.ow, tw);
                         int64_t pick = 0;
                         int pick_band = 0;
@@ -1404,7 +1409,7 @@ void Gpu::build_launches(const mx_plan_desc *p, const std::vector<int64_t> &woff
                         if (pick == 0) continue;
                         Resize2Args r{B(o.src), B(o.dst), X(i, 0), X(i, 1), (int32_t)o.h, (int32_t)o.wd,
                                       (int32_t)o.oh, (int32_t)o.ow, maxt[i][0], maxt[i][1], (int32_t)pick,
-                                      (int32_t)tiles_x, pick_band, span};
+                                      (int32_t)tiles_x, pick_band, span, vec ? 1 : 0, 0};
                         const int mt = std::max(maxt[i][0], maxt[i][1]), ut = mt <= 2 ? 2 : mt <= 4 ? 4 : 8;
                         Launch l = mk(std::string(tw == 256 ? "mx_resize_hv4_t" : "mx_resize_hv_t") + std::to_string(ut));
                         l.g[0] = (uint32_t)(tiles_x * cdiv(o.oh, pick));

@@ -119,6 +119,7 @@ struct Resize2Args {
     int32_t mth, mtv;       // taps per table row
     int32_t rows, tiles_x;  // output rows per block, column tiles per row band
     int32_t band, span;     // LDS input rows and columns (the most any block reads)
+    int32_t vec, pad;       // 1: input rows staged with 128-bit loads (wd % 4 == 0, 16-byte aligned x)
 };
 
 // Nearest subsample.

@@ -570,8 +570,10 @@ extern "C" __global__ __launch_bounds__(MXK_BLOCK) void mx_resize_v(ResizeArgs a
 // input rows its outputs read (the vertical taps of its first row through
 // those of its last: `band` rows at most) over the input columns they read
 // (the horizontal taps of its first column through those of its last: `span`
-// at most; the host sizes the dynamic LDS and checks both ranges), with
-// coalesced loads; runs the horizontal pass from there into LDS; and then the
+// at most; the host sizes the dynamic LDS and checks both ranges; with
+// 128-bit loads a row holds up to 6 more columns, from the 16-byte boundary
+// before the first), with coalesced loads; runs the horizontal pass from
+// there into LDS; and then the
 // vertical pass from LDS to the output. Every intermediate value is computed
 // by the same expression as in mx_resize_h, so the result is bit-identical to
 // the two-pass kernels; rows and columns shared by two blocks are simply
@@ -611,25 +613,53 @@ __device__ void resize_hv(const Resize2Args &a) {
     const int xlo = (int)hf[0], xn = (int)hl[0] + (int)hl[1] - xlo;
     for (int q = tid; q < nrow * sv; q += 256) vt[q] = vf[q];
     // the input rows and columns this block reads, eight loads in flight per
-    // thread before any of them is written to LDS
-    const float *src = a.x + ((int64_t)ch * a.h + jlo) * a.wd + xlo;
-    const int total = nr * xn;
-    for (int q0 = tid; q0 < total; q0 += 8 * 256) {
-        float v[8];
-        int at[8];
+    // thread before any of them is written to LDS: 128-bit loads from the
+    // 16-byte boundary at or before the first column (the LDS rows then
+    // start `lead` <= 3 columns early), else one float at a time
+    int lead = 0;
+    if (a.vec) {
+        const int x4 = xlo & ~3;
+        lead = xlo - x4;
+        const int n4 = (lead + xn + 3) >> 2;
+        const float *src = a.x + ((int64_t)ch * a.h + jlo) * a.wd + x4;
+        const int total = nr * n4;
+        for (int q0 = tid; q0 < total; q0 += 8 * 256) {
+            float4 v[8];
+            int at[8];
 #pragma unroll
-        for (int u = 0; u < 8; ++u) {
-            const int q = q0 + u * 256;
-            at[u] = -1;
-            if (q < total) {
-                const int r = q / xn, c = q - r * xn;
-                v[u] = src[(int64_t)r * a.wd + c];
-                at[u] = r * a.span + c;
+            for (int u = 0; u < 8; ++u) {
+                const int q = q0 + u * 256;
+                at[u] = -1;
+                if (q < total) {
+                    const int r = q / n4, c = q - r * n4;
+                    v[u] = ld4(src + (int64_t)r * a.wd + 4 * c);
+                    at[u] = r * a.span + 4 * c;
+                }
             }
-        }
 #pragma unroll
-        for (int u = 0; u < 8; ++u)
-            if (at[u] >= 0) in[at[u]] = v[u];
+            for (int u = 0; u < 8; ++u)
+                if (at[u] >= 0) st4(in + at[u], v[u]);
+        }
+    } else {
+        const float *src = a.x + ((int64_t)ch * a.h + jlo) * a.wd + xlo;
+        const int total = nr * xn;
+        for (int q0 = tid; q0 < total; q0 += 8 * 256) {
+            float v[8];
+            int at[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                const int q = q0 + u * 256;
+                at[u] = -1;
+                if (q < total) {
+                    const int r = q / xn, c = q - r * xn;
+                    v[u] = src[(int64_t)r * a.wd + c];
+                    at[u] = r * a.span + c;
+                }
+            }
+#pragma unroll
+            for (int u = 0; u < 8; ++u)
+                if (at[u] >= 0) in[at[u]] = v[u];
+        }
     }
     __syncthreads();
 
@@ -645,7 +675,7 @@ __device__ void resize_hv(const Resize2Args &a) {
         for (int k = 0; k < MT; ++k) w[k] = k < a.mth ? e[3 + k] : 0.0f;
         const int r0 = TW == 256 ? 0 : wave, dr = TW == 256 ? 1 : 4;
         for (int r = r0; r < nr; r += dr) {
-            const float *sr = in + r * a.span + b;
+            const float *sr = in + r * a.span + lead + b;
             float acc = 0.0f;
 #pragma unroll
             for (int k = 0; k < MT; ++k)
