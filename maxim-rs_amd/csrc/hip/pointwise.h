@@ -316,28 +316,7 @@ __device__ void body(const GemmArgs &a, int ux, int nx, int by) {
         stat(s1.z, s2.z, lmean.z, lrstd.z);
         stat(s1.w, s2.w, lmean.w, lrstd.w);
     }
-    mma(xa, wa, la, ma, true);
-    int s = 1;
-    for (; s + 2 <= nSw; s += 2) {
-        load(s + 1, xa, wa, la, ma);
-        mma(xb, wb, lb, mb, false);
-        load(min(s + 2, nSw - 1), xb, wb, lb, mb);
-        mma(xa, wa, la, ma, false);
-    }
-    if (s < nSw) mma(xb, wb, lb, mb, false);
-
-    __shared__ float red[KS == 1 ? 1 : 4 * NACC * 64];
     const int64_t cbase = (int64_t)b * a.sC;
-    if (KS == 4) {
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-#pragma unroll
-            for (int mt = 0; mt < TMW; ++mt)
-#pragma unroll
-                for (int r = 0; r < 4; ++r)
-                    red[((wave * NACC) + (j * TMW + mt) * 4 + r) * 64 + lane] = acc[j][mt][r];
-        __syncthreads();
-    }
     // Slot k of this lane: (mt, x) = (k / 4, k % 4) with KS = 1, and
     // (k, wave) with KS = 4 (the wave's share of the slots).
     constexpr int NK = KS == 1 ? 4 * TMW : TMW;
@@ -379,6 +358,35 @@ __device__ void body(const GemmArgs &a, int ux, int nx, int by) {
         if (has_r1) o1[buf] = ld4(a.e.r1 + (r1map ? cbase + pb[buf] : at));
         if (has_r2) o2[buf] = ld4(a.e.r2 + at);
     };
+    // A split reduction's wave takes both its slots' operands now, so their
+    // latency hides behind the multiplies and the reduction (measured 2-5%
+    // faster per launch; a whole-reduction wave keeps fetching one slot
+    // ahead in its epilogue, which measured faster there).
+    if (FUSED && KS == 4) {
+        operands(0, 0);
+        if (NK > 1) operands(1, 1);
+    }
+    mma(xa, wa, la, ma, true);
+    int s = 1;
+    for (; s + 2 <= nSw; s += 2) {
+        load(s + 1, xa, wa, la, ma);
+        mma(xb, wb, lb, mb, false);
+        load(min(s + 2, nSw - 1), xb, wb, lb, mb);
+        mma(xa, wa, la, ma, false);
+    }
+    if (s < nSw) mma(xb, wb, lb, mb, false);
+
+    __shared__ float red[KS == 1 ? 1 : 4 * NACC * 64];
+    if (KS == 4) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int mt = 0; mt < TMW; ++mt)
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+                    red[((wave * NACC) + (j * TMW + mt) * 4 + r) * 64 + lane] = acc[j][mt][r];
+        __syncthreads();
+    }
     // LNO: the wave whose tile is the output LayerNorm's channels keeps its
     // final values for it (and stores them raw only when asked to): with
     // KS = 1 in its own rows of LDS at once, with KS = 4 (where LDS still
@@ -390,11 +398,11 @@ __device__ void body(const GemmArgs &a, int ux, int nx, int by) {
     const int lnspan = (KS == 1 ? a.lo.group : 1) * TW * a.lo.nband;  // rows with a LayerNorm
     const bool lnw = LNO && w0 >= a.lo.row0 && w0 < a.lo.row0 + lnspan;
     float4 vs[LNO && KS == 4 ? NK : 1];
-    if (FUSED) operands(0, 0);
+    if (FUSED && KS == 1) operands(0, 0);
 #pragma unroll
     for (int k = 0; k < NK; ++k) {
         if (LNO && KS == 4) vs[k] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-        if (FUSED && k + 1 < NK) operands(k + 1, (k + 1) & 1);
+        if (FUSED && k + 1 < NK && (KS == 1 || k + 1 > 1)) operands(k + 1, (k + 1) & 1);
         const int mt = KS == 1 ? k / 4 : k, x = KS == 1 ? k % 4 : wave;
         // Out-of-range slots run the arithmetic on clamped operands and skip
         // only the global stores, so the uniform branches below stay
