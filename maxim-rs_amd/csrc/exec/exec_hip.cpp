@@ -301,12 +301,14 @@ struct ConvCfg {
 
 // The Winograd F(2x2, 3x3) kernels (wino.h) take 3x3 convs of at least 8
 // input channels (a multiple of 8) and 32 output channels, in blocks of 32
-// output channels x 4 x TC tiles: TC = 8 (8 x 16 pixels) where that fills
-// the chip four blocks deep, else 4 (8 x 8).
-int pick_wino(int64_t ci, int64_t co, int64_t h, int64_t w, int cus) {
+// output channels x 4 x TC tiles: TC = 8 (8 x 16 pixels) where the width
+// allows, else 4 (8 x 8). A block reads its 32 channels' transformed filters
+// once per tile grid, so the wider grid halves that traffic; at 112x160 (128
+// channels, 560 blocks, not enough to fill the chip four deep) TC = 8 still
+// measured 48.3 -> 37.6 us per launch.
+int pick_wino(int64_t ci, int64_t co, int64_t h, int64_t w) {
     if (ci < 8 || ci % 8 || co < 32 || w % 4 || 8 * h * w >= (1LL << 31)) return 0;
-    const int64_t mb = (co + 31) / 32, slots = 4LL * (cus > 0 ? cus : 256);
-    if (w % 16 == 0 && ((h + 7) / 8) * (w / 16) * mb >= slots) return 8;
+    if (w % 16 == 0) return 8;
     return w % 8 == 0 ? 4 : 0;
 }
 
@@ -909,7 +911,7 @@ void Gpu::init(const mx_plan_desc *p) {
                     extra[i][3] = placev(q);
                 }
                 if (k3 && !std::getenv("MAXIM_NO_WINOGRAD")) {
-                    ccfg[i].wtc = pick_wino(o.c_in, o.c_out, o.h, o.wd, cus);
+                    ccfg[i].wtc = pick_wino(o.c_in, o.c_out, o.h, o.wd);
                     if (ccfg[i].wtc) extra[i][2] = placev(wino_weights(w, o.c_out, o.c_in));
                 }
                 as_is(o.bias);
@@ -2980,6 +2982,18 @@ void Gpu::pair_launches(const mx_plan_desc *p) {
 // where the code object has one: the same arithmetic in the same order,
 // without the per-slot tests of the argument block.
 void Gpu::specialise(Launch &l) {
+    if (l.kind == 2 && !strncmp(l.name, "mx_wino3_", 9)) {
+        // the Winograd conv's fused epilogue when it is a LeakyReLU alone
+        const size_t n = strlen(l.name);
+        if (n < 2 || strcmp(l.name + n - 2, "_f")) return;
+        ConvArgs a;
+        memcpy(&a, l.a0, sizeof a);
+        if (a.e.u || a.e.m || a.e.r1 || a.e.r2 || a.e.act != MXK_ACT_LRELU) return;
+        const std::string sn = std::string(l.name) + "_e16";
+        l.name = intern(sn);
+        l.f = fn(l.name);
+        return;
+    }
     if (l.kind != 1 || strncmp(l.name, "mx_pw_", 6)) return;
     const std::string nm = l.name;
     auto ends = [&](const char *t) {

@@ -75,6 +75,33 @@ __device__ __forceinline__ float epilogue(const Epilogue &e, float v, int64_t id
     return v;
 }
 
+// The same for the two elements idx, idx + 1, with 64-bit operand loads
+// (idx even and every operand 8-byte aligned): each element's operations and
+// their order are epilogue()'s.
+__device__ __forceinline__ void epilogue2(const Epilogue &e, float &v0, float &v1, int64_t idx) {
+    const float2 zero = make_float2(0.0f, 0.0f);
+    const float2 u2 = e.u ? *reinterpret_cast<const float2 *>(e.u + idx) : zero;
+    const float2 m2 = e.m ? *reinterpret_cast<const float2 *>(e.m + idx) : zero;
+    const float2 a2 = e.r1 ? *reinterpret_cast<const float2 *>(e.r1 + idx) : zero;
+    const float2 b2 = e.r2 ? *reinterpret_cast<const float2 *>(e.r2 + idx) : zero;
+    const float uu[2] = {u2.x, u2.y}, mm[2] = {m2.x, m2.y}, aa[2] = {a2.x, a2.y}, bb[2] = {b2.x, b2.y};
+    float v[2] = {v0, v1};
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+        float x = v[k];
+        if (e.u) x = uu[k] * (x + 1.0f);
+        if (e.act == MXK_ACT_GELU) x = gelu(x);
+        else if (e.act == MXK_ACT_LRELU) x = x >= 0.0f ? x : e.slope * x;
+        else if (e.act == MXK_ACT_SIGMOID) x = sigmoid(x);
+        if (e.m) x = x * mm[k];
+        if (e.r1) x = x + aa[k];
+        if (e.r2) x = x + bb[k];
+        v[k] = x;
+    }
+    v0 = v[0];
+    v1 = v[1];
+}
+
 // The same for the four elements idx .. idx + 3, with 128-bit operand loads
 // (idx % 4 == 0 and every operand 16-byte aligned): each element's operations
 // and their order are epilogue()'s.

@@ -37,7 +37,9 @@ constexpr int BM = 32;  // output channels per block
 constexpr int CK = 8;   // input channels per chunk
 constexpr int TR = 4;   // tile rows per block (8 output rows)
 
-template <int TC, bool FUSED>
+// EP: -1 the generic fused epilogue, 16 a LeakyReLU only (the residual
+// blocks' first conv; the same expression as the generic one).
+template <int TC, bool FUSED, int EP = -1>
 __device__ void body(const ConvArgs &a) {
     constexpr int NT = TR * TC;          // tiles per block
     constexpr int OW = 2 * TC;           // output columns per block
@@ -64,6 +66,15 @@ __device__ void body(const ConvArgs &a) {
     xcd_tile(tile, mb);
     const int oy0 = (tile / tiles_x) * (2 * TR), ox0 = (tile % tiles_x) * OW;
     const int m0 = mb * BM;
+    // the bias of this thread's (output channel, tile) pairs of the
+    // epilogue, fetched now so its latency hides behind the main loop
+    constexpr int PAIRS = BM * NT / 256;
+    float bsv[PAIRS];
+#pragma unroll
+    for (int q = 0; q < PAIRS; ++q) {
+        const int m = m0 + (tid + q * 256) / NT;
+        bsv[q] = a.bias && m < a.co ? a.bias[m] : 0.0f;
+    }
     const int plane = a.h * a.wd;  // 8 planes < 2^31, checked by the host
     const int nchunk = (a.ci + CK - 1) / CK;
     // this block's transformed filters, [chunk][wave][lane][16]
@@ -118,17 +129,12 @@ __device__ void body(const ConvArgs &a) {
             pofs[ks][ni] = c * HH * HP + (t / TC) * 2 * HP + (t % TC) * 2 + 3;
         }
 
-    f32x4 acc[4][2][NI];
-#pragma unroll
-    for (int nu = 0; nu < 4; ++nu)
-#pragma unroll
-        for (int mi = 0; mi < 2; ++mi)
-#pragma unroll
-            for (int ni = 0; ni < NI; ++ni) acc[nu][mi][ni] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    f32x4 acc[4][2][NI];  // set by the first chunk
 
     fetch_halo(0);
     fetch_u(0);
-    for (int chunk = 0; chunk < nchunk; ++chunk) {
+    // first: chunk 0, whose multiplies start from an inline zero
+    auto chunk_step = [&](int chunk, bool first) {
         float *Hs = smem + (chunk & 1) * HALO;
         // (every wave finished reading this buffer two chunks ago, before
         // the previous chunk's barrier)
@@ -162,10 +168,14 @@ __device__ void body(const ConvArgs &a) {
 #pragma unroll
                 for (int mi = 0; mi < 2; ++mi)
 #pragma unroll
-                    for (int ni = 0; ni < NI; ++ni)
-                        acc[nu][mi][ni] = mfma16(uv[(nu * 2 + ks) * 2 + mi], v[ks][ni][nu], acc[nu][mi][ni]);
+                    for (int ni = 0; ni < NI; ++ni) {
+                        const f32x4 c = first && ks == 0 ? f32x4{0.0f, 0.0f, 0.0f, 0.0f} : acc[nu][mi][ni];
+                        acc[nu][mi][ni] = mfma16(uv[(nu * 2 + ks) * 2 + mi], v[ks][ni][nu], c);
+                    }
         if (chunk + 1 < nchunk) fetch_u(chunk + 1);
-    }
+    };
+    chunk_step(0, true);
+    for (int chunk = 1; chunk < nchunk; ++chunk) chunk_step(chunk, false);
 
     // (.) A over nu in registers: u[dx] for this wave's transform row xi;
     // then the rows of all four waves meet in LDS as Ms[xi][dx][m][t].
@@ -184,8 +194,10 @@ __device__ void body(const ConvArgs &a) {
             }
     __syncthreads();
     // A^T . over xi, bias, epilogue, stores: thread -> (m, tile), tiles fastest
+    // The host launches whole tiles along x (ow % 2 TC == 0), so each
+    // pair's second column is inside the image; rows may be ragged.
     const int64_t oplane = (int64_t)a.oh * a.ow;
-    constexpr int PAIRS = BM * NT / 256;
+    const bool vec = a.cvec != 0;
 #pragma unroll
     for (int q = 0; q < PAIRS; ++q) {
         const int e = tid + q * 256, m = e / NT, t = e % NT;
@@ -202,21 +214,27 @@ __device__ void body(const ConvArgs &a) {
             y[1][dx] = u[1][dx] - u[2][dx] - u[3][dx];
         }
         const int oy = oy0 + 2 * (t / TC), ox = ox0 + 2 * (t % TC);
-        const float bb = a.bias ? a.bias[m0 + m] : 0.0f;
+        const int64_t ib = (int64_t)(m0 + m) * oplane + ox;
+        const float bb = bsv[q];
 #pragma unroll
         for (int dy = 0; dy < 2; ++dy) {
             if (oy + dy >= a.oh) continue;
-            const int64_t idx = (int64_t)(m0 + m) * oplane + (int64_t)(oy + dy) * a.ow + ox;
+            const int64_t idx = ib + (int64_t)(oy + dy) * a.ow;
             float v0 = bb + y[dy][0], v1 = bb + y[dy][1];
-            if (FUSED) {
-                v0 = epilogue(a.e, v0, idx);
-                if (ox + 1 < a.ow) v1 = epilogue(a.e, v1, idx + 1);
+            if (EP == 16) {
+                v0 = v0 >= 0.0f ? v0 : a.e.slope * v0;
+                v1 = v1 >= 0.0f ? v1 : a.e.slope * v1;
             }
-            if (ox + 1 < a.ow && a.cvec) {
+            if (vec) {
+                if (FUSED && EP < 0) epilogue2(a.e, v0, v1, idx);
                 *reinterpret_cast<float2 *>(a.y + idx) = make_float2(v0, v1);
             } else {
-                if (ox < a.ow) a.y[idx] = v0;
-                if (ox + 1 < a.ow) a.y[idx + 1] = v1;
+                if (FUSED && EP < 0) {
+                    v0 = epilogue(a.e, v0, idx);
+                    v1 = epilogue(a.e, v1, idx + 1);
+                }
+                a.y[idx] = v0;
+                a.y[idx + 1] = v1;
             }
         }
     }
@@ -226,15 +244,19 @@ __device__ void body(const ConvArgs &a) {
 
 // mx_wino3_t<TC>[_f]: 3x3 pad 1 by F(2x2, 3x3), 32 output channels x 4 x TC
 // tiles (8 x 2TC pixels) per block; _f applies the fused epilogue. The host
-// guarantees: input rows 16-byte aligned (width % 4 == 0, aligned base),
-// output width a multiple of 2 TC, and 8-byte aligned output rows for the
-// paired stores (cvec).
+// guarantees: input rows 16-byte aligned (width % 4 == 0, aligned base) and
+// output width a multiple of 2 TC; cvec: the output and every epilogue
+// operand 8-byte aligned (paired loads and stores). _f_e16: the fused
+// epilogue when it is a LeakyReLU alone.
 #define MXK_WINO(TC)                                                                               \
     extern "C" __global__ __launch_bounds__(256) void mx_wino3_t##TC(ConvArgs a) {                  \
         wino::body<TC, false>(a);                                                                  \
     }                                                                                              \
     extern "C" __global__ __launch_bounds__(256) void mx_wino3_t##TC##_f(ConvArgs a) {              \
         wino::body<TC, true>(a);                                                                   \
+    }                                                                                              \
+    extern "C" __global__ __launch_bounds__(256) void mx_wino3_t##TC##_f_e16(ConvArgs a) {          \
+        wino::body<TC, true, 16>(a);                                                               \
     }
 MXK_WINO(8)
 MXK_WINO(4)

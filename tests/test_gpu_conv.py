@@ -14,7 +14,7 @@ def expect_kernel(ci, co, h, w):
     if co <= 4 and ci >= 64:
         return "mx_conv3x3_co4"
     if ci >= 8 and ci % 8 == 0 and co >= 32 and w % 8 == 0:
-        return "mx_wino3_t8" if w % 16 == 0 and ((h + 7) // 8) * (w // 16) * ((co + 31) // 32) >= 1024 else "mx_wino3_t4"
+        return "mx_wino3_t8" if w % 16 == 0 else "mx_wino3_t4"
     if ci % 16 == 0 and ci >= 128:
         return "mx_c3_"
     return "mx_conv3x3v_" if w % 16 == 0 else "mx_conv3x3_"
@@ -78,8 +78,8 @@ def test_conv3x3_lrelu_fused(gpu_ok, misalign):
     assert (int(cp.offs[3]) % 4 != 0) == bool(misalign)
     got, steps = run_plan(cp, {0: x}, 3)
     print("steps", steps)
-    assert len(steps) == 1 and steps[0][2].endswith("_f")
-    assert steps[0][2].startswith("mx_wino3_")
+    # the LeakyReLU-only specialisation of the Winograd kernel's epilogue
+    assert len(steps) == 1 and steps[0][2].startswith("mx_wino3_") and steps[0][2].endswith("_f_e16")
     check(got, oracle_plan(cp, {0: x}, 3), "conv3x3 + lrelu, output misaligned %d" % misalign)
 
 
