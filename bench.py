@@ -395,6 +395,12 @@ def launch_costs(plan, steps, launches, R, spans=None):
                 else:
                     out[i] = (2 * c.c_in * c.c_out * pl, 4 * (c.c_in * pl + c.c_out * pl + c.c_in * c.c_out + bias))
             continue
+        if o.kind == P.CONV4X4S2 and len(idx) == 2:
+            # a split-reduction 4x4: the slices carry the op's work, their
+            # sum (mx_conv_split_sum) moves only partials
+            for i, kn in zip(idx, names):
+                out[i] = step_cost(a, b) if kn.startswith("mx_conv4x4") else (0, 0)
+            continue
         for i, kn in zip(idx, names):
             if kn.startswith("mx_chan_ln_stats"):
                 out[i] = (0, 4 * (o.c * o.hw + 2 * o.hw))

@@ -297,6 +297,7 @@ struct ConvCfg {
     int bm = 0, th = 0, ck = 0;
     int c3bm = 0, c3th = 0;  // the mx_c3 tile, when the op qualifies for it
     int wtc = 0;             // the Winograd kernel's tile columns (4 or 8), 0: not eligible
+    int nsplit = 1;          // 4x4: slices of the split reduction (mx_conv4x4_*_s)
 };
 
 // The Winograd F(2x2, 3x3) kernels (wino.h) take 3x3 convs of at least 8
@@ -372,6 +373,20 @@ ConvCfg pick_conv(int64_t co, int64_t ci, int64_t oh, int64_t ow, bool k3, int c
         }
     }
     r.ck = (k3 && ci > 4) ? 8 : 4;
+    if (!k3) {
+        // A 4x4 whose blocks do not fill the chip twice splits its reduction
+        // over 2 or 4 z-slices of at least four chunks each (partial outputs
+        // in scratch, then mx_conv_split_sum): at 112x160 and 56x80 (64 and
+        // 128 channels, 280 blocks) one slice per block leaves most CUs idle.
+        const int64_t blocks = ((co + r.bm - 1) / r.bm) * ((oh + r.th - 1) / r.th) * ((ow + 15) / 16);
+        const int64_t nchunk = (ci + 3) / 4;
+        if (blocks < slots && (oh * ow) % 4 == 0)
+            for (int s : {4, 2})
+                if (nchunk % s == 0 && nchunk / s >= 4 && blocks * s <= 5 * slots / 2) {
+                    r.nsplit = s;
+                    break;
+                }
+    }
     if (k3 && ci > 4) {
         // measured on MI355X at the MAXIM shapes (c -> c, 32 to 128 channels):
         // 32-channel blocks of 8 rows for narrow outputs, 64 x 4 up to 64
@@ -458,7 +473,7 @@ public:
     unsigned char *wdev = nullptr;
     uint64_t wbytes = 0;
     float *scratch = nullptr;
-    uint64_t scratch_len = 0, ln_off = 0, so_base = 0, rs_off = 0;
+    uint64_t scratch_len = 0, ln_off = 0, so_base = 0, rs_off = 0, cs_off = 0;
     uint64_t n_ops = 0, n_bufs = 0;
     std::vector<std::vector<Launch>> ops;
     uint64_t launched = 0, kernels = 0;
@@ -1006,7 +1021,13 @@ void Gpu::init(const mx_plan_desc *p) {
             rs_need = std::max<uint64_t>(rs_need, (uint64_t)(c.c_out * r.h * r.wd));
         }
     rs_off = (so_base + pg.so_len + 63) & ~(uint64_t)63;
-    scratch_len = std::max<uint64_t>(rs_off + rs_need, 64);
+    // then the partial outputs of split-reduction 4x4 convs (one op at a time)
+    uint64_t cs_need = 0;
+    for (uint64_t i = 0; i < p->n_ops; ++i)
+        if (p->ops[i].kind == MX_OP_CONV4X4S2 && ccfg[i].nsplit > 1)
+            cs_need = std::max<uint64_t>(cs_need, (uint64_t)(ccfg[i].nsplit * p->ops[i].c_out * p->ops[i].oh * p->ops[i].ow));
+    cs_off = (rs_off + rs_need + 63) & ~(uint64_t)63;
+    scratch_len = std::max<uint64_t>(cs_off + cs_need, 64);
     const uint64_t need = arena_len * 4 + wbytes + scratch_len * 4;
     size_t free_b = 0, total_b = 0;
     if (H.hipMemGetInfo(&free_b, &total_b) == 0 && need > free_b) {
@@ -1215,6 +1236,28 @@ void Gpu::build_launches(const mx_plan_desc *p, const std::vector<int64_t> &woff
                 l.g[1] = grid_yz((o.c_out + cc.bm - 1) / cc.bm);
                 set_args(l, a);
                 l.kind = 2;
+                if (!k3 && cc.nsplit > 1 && aligned(a.y, 16)) {
+                    // the reduction in z-slices into scratch, then their sum
+                    ConvArgs b = a;
+                    b.y = scratch + cs_off;
+                    b.bias = nullptr;
+                    b.cvec = a.ow % 4 == 0;
+                    b.ksplit = (int32_t)((o.c_in + 3) / 4 / cc.nsplit);
+                    Launch q = mk(cn + "_s");
+                    q.g[0] = l.g[0];
+                    q.g[1] = l.g[1];
+                    q.g[2] = (unsigned)cc.nsplit;
+                    set_args(q, b);
+                    q.kind = 2;
+                    const int64_t n = o.c_out * o.oh * o.ow;
+                    ConvSumArgs sa{scratch + cs_off, a.bias, a.y, n, o.oh * o.ow, cc.nsplit, 0};
+                    Launch r = mk("mx_conv_split_sum");
+                    r.g[0] = cdiv(n / 4, 256);
+                    set_args(r, sa);
+                    L.push_back(q);
+                    L.push_back(r);
+                    break;
+                }
                 if (k3 && o.c_out <= 4 && o.c_in >= 64) {
                     // at most four outputs from many inputs: the vector-ALU
                     // kernel (measured faster than 16-channel MFMA blocks

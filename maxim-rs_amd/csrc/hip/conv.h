@@ -24,7 +24,11 @@ namespace conv {
 // thread's row, column and channel offsets fixed for the block, and stored
 // in LDS rows of HP = 24 floats with the tile's columns at 4..19 (16-byte
 // aligned), the left edge at 3 and the right edge at 20.
-template <int BM, int TH, int TW, int CK, int KS, int STRIDE, int WAVES_M, int WAVES_N, bool FUSED, bool XV = false>
+// SPLIT: the reduction over input channels is split along the grid's z
+// (a.ksplit chunks per slice); each slice writes its raw partial sums, no
+// bias, to slice z of a.y ([z][co][oh][ow]), for mx_conv_split_sum.
+template <int BM, int TH, int TW, int CK, int KS, int STRIDE, int WAVES_M, int WAVES_N, bool FUSED, bool XV = false,
+          bool SPLIT = false>
 __device__ void body(const ConvArgs &a) {
     constexpr int TAPS = KS * KS;
     constexpr int KC = TAPS * CK;
@@ -141,8 +145,10 @@ __device__ void body(const ConvArgs &a) {
 #pragma unroll
         for (int j = 0; j < TN; ++j) acc[i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 
-    fetch(0);
-    for (int chunk = 0; chunk < nchunk; ++chunk) {
+    const int cbeg = SPLIT ? (int)blockIdx.z * a.ksplit : 0;
+    const int cend = SPLIT ? min(nchunk, cbeg + a.ksplit) : nchunk;
+    fetch(cbeg);
+    for (int chunk = cbeg; chunk < cend; ++chunk) {
         __syncthreads();
 #pragma unroll
         for (int i = 0; i < NW; ++i) {
@@ -162,7 +168,7 @@ __device__ void body(const ConvArgs &a) {
             }
         }
         __syncthreads();
-        if (chunk + 1 < nchunk) fetch(chunk + 1);
+        if (chunk + 1 < cend) fetch(chunk + 1);
         // k = kk + lk: tap kk / CK (CK % 4 == 0), channel kk % CK + lk
 #pragma unroll
         for (int kk = 0; kk < KC; kk += 4) {
@@ -182,6 +188,7 @@ __device__ void body(const ConvArgs &a) {
     // Stage each 16-channel slab of the wave's tile in LDS and write it out as
     // rows of four adjacent output pixels per lane.
     const int64_t oplane = (int64_t)a.oh * a.ow;
+    float *yout = SPLIT ? a.y + (int64_t)blockIdx.z * a.co * oplane : a.y;
     __syncthreads();
     float *sw = smem + wave * (16 * LDS);
     constexpr int PER = 16 * WTN / 4 / 64;
@@ -211,7 +218,7 @@ __device__ void body(const ConvArgs &a) {
             const int64_t idx = m * oplane + (int64_t)oy * a.ow + ox;
 #pragma unroll
             for (int u = 0; u < 4; ++u)
-                if (a.bias) v[u] = a.bias[m] + v[u];
+                if (a.bias && !SPLIT) v[u] = a.bias[m] + v[u];
             if (FUSED) {
                 // (past the row's end there is nothing to read: the lanes
                 // of a ragged last column group skip those elements)
@@ -224,11 +231,11 @@ __device__ void body(const ConvArgs &a) {
                 }
             }
             if (a.cvec && ox + 3 < a.ow) {
-                st4(a.y + idx, make_float4(v[0], v[1], v[2], v[3]));
+                st4(yout + idx, make_float4(v[0], v[1], v[2], v[3]));
             } else {
 #pragma unroll
                 for (int u = 0; u < 4; ++u)
-                    if (ox + u < a.ow) a.y[idx + u] = v[u];
+                    if (ox + u < a.ow) yout[idx + u] = v[u];
             }
         }
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -278,11 +285,14 @@ MXK_CONV3(32, 4, 4, 2, 2, _c4)
 MXK_CONV3(64, 4, 4, 2, 2, _c4)
 MXK_CONV3(128, 4, 4, 4, 1, _c4)
 
-// mx_conv4x4_m<BM>_t<TH>: 4x4 stride 2 SAME, CK = 4, TH x 16 outputs over a
-// (2 TH + 2) x 34 input halo.
+// mx_conv4x4_m<BM>_t<TH>[_s]: 4x4 stride 2 SAME, CK = 4, TH x 16 outputs
+// over a (2 TH + 2) x 34 input halo; _s: the reduction split along z.
 #define MXK_CONV4(BM, TH, WM, WN)                                                               \
     extern "C" __global__ __launch_bounds__(256) void mx_conv4x4_m##BM##_t##TH(ConvArgs a) {    \
         conv::body<BM, TH, 16, 4, 4, 2, WM, WN, false>(a);                                      \
+    }                                                                                           \
+    extern "C" __global__ __launch_bounds__(256) void mx_conv4x4_m##BM##_t##TH##_s(ConvArgs a) { \
+        conv::body<BM, TH, 16, 4, 4, 2, WM, WN, false, false, true>(a);                         \
     }
 MXK_CONV4(32, 8, 1, 4)
 MXK_CONV4(64, 8, 2, 2)
@@ -369,3 +379,26 @@ __device__ void co4(const ConvArgs &a) {
 // [c_in][9][4], zero beyond c_out), one 8 x 8 output tile per block.
 extern "C" __global__ __launch_bounds__(256) void mx_conv3x3_co4(ConvArgs a) { conv::co4<false>(a); }
 extern "C" __global__ __launch_bounds__(256) void mx_conv3x3_co4_f(ConvArgs a) { conv::co4<true>(a); }
+
+// y = bias + the z-ordered sum of a split-reduction conv's partial outputs
+// (ConvSumArgs), four elements per thread.
+extern "C" __global__ __launch_bounds__(256) void mx_conv_split_sum(ConvSumArgs a) {
+    const int64_t i = 4 * ((int64_t)blockIdx.x * 256 + threadIdx.x);
+    if (i >= a.n) return;
+    float4 s = ld4(a.part + i);
+    for (int z = 1; z < a.nsplit; ++z) {
+        const float4 t = ld4(a.part + (int64_t)z * a.n + i);
+        s.x = s.x + t.x;
+        s.y = s.y + t.y;
+        s.z = s.z + t.z;
+        s.w = s.w + t.w;
+    }
+    if (a.bias) {
+        const float b = a.bias[i / a.plane];
+        s.x = b + s.x;
+        s.y = b + s.y;
+        s.z = b + s.z;
+        s.w = b + s.w;
+    }
+    st4(a.y + i, s);
+}

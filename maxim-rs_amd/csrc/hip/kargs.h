@@ -243,6 +243,18 @@ struct ConvArgs {
     float *y;
     int32_t ci, co, h, wd;
     int32_t oh, ow, pad_top, pad_left;
-    int32_t cvec, pad;    // 1: y, u, r1, r2 are 16-byte aligned and ow % 4 == 0
+    int32_t cvec;         // 1: y, u, r1, r2 are 16-byte aligned and ow % 4 == 0
+    int32_t ksplit;       // split reduction (_s kernels): input-channel chunks per z-slice
     Epilogue e;
+};
+
+// The sum of a split-reduction conv's partial outputs, in z order, plus the
+// bias: y[m][p] = b[m] + (((part[0] + part[1]) + ...) + part[S - 1]).
+struct ConvSumArgs {
+    const float *part;  // [nsplit][n]
+    const float *bias;
+    float *y;
+    int64_t n;          // co * oh * ow, a multiple of 4
+    int64_t plane;      // oh * ow, a multiple of 4
+    int32_t nsplit, pad;
 };

@@ -144,3 +144,41 @@ def test_conv3x3_add_fused(gpu_ok, ci, h, w):
     assert len(steps) == 1 and steps[0][2].endswith("_f"), steps
     assert np.array_equal(got.view(np.uint32), unfused(cp, inputs, 3).view(np.uint32))
     check(got, oracle_plan(cp, inputs, 3), "conv3x3 %d->3 + image @%dx%d" % (ci, h, w))
+
+
+@pytest.mark.parametrize("ci,co,h,w,split", [
+    (64, 64, 224, 320, True),    # the C4 112x160 downsampling: 280 blocks, four slices of four chunks
+    (128, 128, 112, 160, True),  # the C4 56x80 one: four slices of eight chunks
+    (128, 96, 40, 36, True),     # a partial channel block, output rows not a multiple of 4 wide
+    (32, 32, 448, 640, False),   # the C4 224x320 one fills the chip unsplit
+    (64, 32, 30, 38, False),     # 15x19 outputs: a plane not a multiple of 4
+])
+def test_conv4x4_split_reduction(gpu_ok, ci, co, h, w, split):
+    """4x4 stride-2 convs whose blocks do not fill the chip split the input
+    channels over z-slices (partial outputs in scratch) and sum the slices in
+    z order with the bias (mx_conv_split_sum); within the GEMM bar of the CPU
+    path either way."""
+    from maxim_amd import plan as P
+    from maxim_amd import hip as H
+    from oracle import oracle as O
+    rng = np.random.default_rng(ci + co + h)
+    x = rng.standard_normal((ci, h, w)).astype(np.float32)
+    wt = he(rng, (co, ci, 4, 4), 16 * ci)
+    b = (rng.standard_normal(co) * 0.1).astype(np.float32)
+    pt, _ = P.same_pad(h, 2, 4)
+    pl, _ = P.same_pad(w, 2, 4)
+    oh, ow = (h + 1) // 2, (w + 1) // 2
+    op = P.make_op(P.CONV4X4S2, dst=1, src=0, w=0, bias=1, c_in=ci, c_out=co, h=h, wd=w, oh=oh, ow=ow, p=[pt, pl])
+    cp = P.CustomPlan([(ci, h, w), (co, oh, ow)], [op], [wt, b], input=0, output=1)
+    gpu = H.Gpu(cp)
+    gpu.write_buf(0, x)
+    gpu.run_ops(0, 1)
+    got = gpu.read_buf(1).reshape(co, oh, ow)
+    ks = [k for _, k in gpu.launches()]
+    gpu.close()
+    print(ks)
+    if split:
+        assert len(ks) == 2 and ks[0].startswith("mx_conv4x4_") and ks[0].endswith("_s") and ks[1] == "mx_conv_split_sum", ks
+    else:
+        assert len(ks) == 1 and ks[0].startswith("mx_conv4x4_") and not ks[0].endswith("_s"), ks
+    check(got, O.conv4x4s2(x, wt, b, pt, pl), "conv4x4s2 %d->%d @%dx%d" % (ci, co, h, w))
