@@ -302,13 +302,15 @@ struct ConvCfg {
 
 // The Winograd F(2x2, 3x3) kernels (wino.h) take 3x3 convs of at least 8
 // input channels (a multiple of 8) and 32 output channels, in blocks of 32
-// output channels x 4 x TC tiles: TC = 8 (8 x 16 pixels) where the width
-// allows, else 4 (8 x 8). A block reads its 32 channels' transformed filters
-// once per tile grid, so the wider grid halves that traffic; at 112x160 (128
-// channels, 560 blocks, not enough to fill the chip four deep) TC = 8 still
-// measured 48.3 -> 37.6 us per launch.
+// output channels x TR x TC tiles: TC = 16 (4 x 32 pixels) where the width
+// allows, else 8 (8 x 16), else 4 (8 x 8). A block reads its 32 channels'
+// transformed filters once per tile grid, so the 32-tile grids halve that
+// traffic against 8 x 8 (at 112x160, 128 channels, 48.3 -> 37.6 us per
+// launch), and 32-pixel rows move 128-byte runs of each plane instead of
+// 64-byte ones (37.6 -> 36.5 us).
 int pick_wino(int64_t ci, int64_t co, int64_t h, int64_t w) {
     if (ci < 8 || ci % 8 || co < 32 || w % 4 || 8 * h * w >= (1LL << 31)) return 0;
+    if (w % 32 == 0) return 16;
     if (w % 16 == 0) return 8;
     return w % 8 == 0 ? 4 : 0;
 }
@@ -1271,12 +1273,13 @@ void Gpu::build_launches(const mx_plan_desc *p, const std::vector<int64_t> &woff
                     alt[i].push_back(l);
                     L.push_back(q);
                 } else if (k3 && cc.wtc && aligned(a.x, 16)) {
-                    // Winograd F(2x2, 3x3): 32 output channels x 4 x TC tiles
+                    // Winograd F(2x2, 3x3): 32 output channels x TR x TC tiles
                     ConvArgs b = a;
                     b.w = X(i, 2);
                     b.cvec = aligned(a.y, 8) && a.ow % 2 == 0;
                     Launch q = mk("mx_wino3_t" + std::to_string(cc.wtc));
-                    q.g[0] = cdiv((int64_t)((a.oh + 7) / 8) * ((a.ow + 2 * cc.wtc - 1) / (2 * cc.wtc)), 1);
+                    const int trows = cc.wtc == 16 ? 4 : 8;  // output rows per block
+                    q.g[0] = cdiv((int64_t)((a.oh + trows - 1) / trows) * ((a.ow + 2 * cc.wtc - 1) / (2 * cc.wtc)), 1);
                     q.g[1] = grid_yz((o.c_out + 31) / 32);
                     set_args(q, b);
                     q.kind = 2;

@@ -12,9 +12,9 @@
 //   G   = [1 0 0; 1/2 1/2 1/2; 1/2 -1/2 1/2; 0 0 1]
 //   A^T = [1 1 1 0; 0 1 -1 -1]
 //
-// A block owns 32 output channels x a 4 x TC grid of tiles (8 x 2TC output
-// pixels) and walks the input channels in chunks of 8. Per chunk the input
-// halo (10 x (2TC + 2) per channel) is staged in LDS (128-bit loads of the
+// A block owns 32 output channels x a TR x TC grid of tiles (2TR x 2TC output
+// pixels: 8 x 8, 8 x 16 or 4 x 32) and walks the input channels in chunks of
+// 8. Per chunk the input halo ((2TR + 2) x (2TC + 2) per channel) is staged in LDS (128-bit loads of the
 // tile's columns, the two edge columns as scalars; two buffers, so one block
 // barrier per chunk). Wave w owns the transform row xi = w (positions
 // p = 4w + nu, nu = 0..3), and each of its lanes transforms exactly the
@@ -35,12 +35,12 @@ namespace wino {
 
 constexpr int BM = 32;  // output channels per block
 constexpr int CK = 8;   // input channels per chunk
-constexpr int TR = 4;   // tile rows per block (8 output rows)
 
 // EP: -1 the generic fused epilogue, 16 a LeakyReLU only (the residual
 // blocks' first conv; the same expression as the generic one).
 template <int TC, bool FUSED, int EP = -1>
 __device__ void body(const ConvArgs &a) {
+    constexpr int TR = TC == 16 ? 2 : 4;  // tile rows per block
     constexpr int NT = TR * TC;          // tiles per block
     constexpr int OW = 2 * TC;           // output columns per block
     constexpr int HH = 2 * TR + 2;       // halo rows
@@ -53,7 +53,7 @@ __device__ void body(const ConvArgs &a) {
     constexpr int HALO = CK * HH * HP;
     constexpr int MS = 4 * 2 * BM * MP;
     constexpr int POOL = 2 * HALO > MS ? 2 * HALO : MS;
-    static_assert(TC == 8 || TC == 4, "4 x 8 or 4 x 4 tiles");
+    static_assert(TC == 16 || TC == 8 || TC == 4, "2 x 16, 4 x 8 or 4 x 4 tiles");
     static_assert(NE <= 256, "one edge per thread");
     __shared__ float smem[POOL];
     float *Ms = smem;
@@ -242,8 +242,8 @@ __device__ void body(const ConvArgs &a) {
 
 }  // namespace wino
 
-// mx_wino3_t<TC>[_f]: 3x3 pad 1 by F(2x2, 3x3), 32 output channels x 4 x TC
-// tiles (8 x 2TC pixels) per block; _f applies the fused epilogue. The host
+// mx_wino3_t<TC>[_f]: 3x3 pad 1 by F(2x2, 3x3), 32 output channels x TR x TC
+// tiles (TR = 2 for TC = 16, else 4) per block; _f applies the fused epilogue. The host
 // guarantees: input rows 16-byte aligned (width % 4 == 0, aligned base) and
 // output width a multiple of 2 TC; cvec: the output and every epilogue
 // operand 8-byte aligned (paired loads and stores). _f_e16: the fused
@@ -258,5 +258,6 @@ __device__ void body(const ConvArgs &a) {
     extern "C" __global__ __launch_bounds__(256) void mx_wino3_t##TC##_f_e16(ConvArgs a) {          \
         wino::body<TC, true, 16>(a);                                                               \
     }
+MXK_WINO(16)
 MXK_WINO(8)
 MXK_WINO(4)

@@ -53,7 +53,7 @@ def test_the_code_object_is_embedded_and_complete():
                  for s in ("", "_c4") for f in ("", "_f")}
     launched |= {"mx_conv4x4_m%d_t%d%s" % (m, t, z) for m in (32, 64, 128) for t in (4, 8) for z in ("", "_s")}
     launched |= {"mx_conv3x3%s_m16_t8%s" % (v, f) for v in ("", "v") for f in ("", "_f")}
-    launched |= {"mx_wino3_t%d%s" % (t, f) for t in (4, 8) for f in ("", "_f", "_f_e16")}
+    launched |= {"mx_wino3_t%d%s" % (t, f) for t in (4, 8, 16) for f in ("", "_f", "_f_e16")}
     launched |= {"mx_conv3x3v_m%d_t%d%s" % (m, t, f) for m in (32, 64, 128) for t in (4, 8) for f in ("", "_f")}
     launched |= {"mx_pw_%s%d%s%s" % (l, t, k, f) for l in ("ch", "rw") for t in (1, 2, 4)
                  for k in ("", "_k4") for f in ("", "_f")}

@@ -14,7 +14,7 @@ def expect_kernel(ci, co, h, w):
     if co <= 4 and ci >= 64:
         return "mx_conv3x3_co4"
     if ci >= 8 and ci % 8 == 0 and co >= 32 and w % 8 == 0:
-        return "mx_wino3_t8" if w % 16 == 0 else "mx_wino3_t4"
+        return "mx_wino3_t16" if w % 32 == 0 else "mx_wino3_t8" if w % 16 == 0 else "mx_wino3_t4"
     if ci % 16 == 0 and ci >= 128:
         return "mx_c3_"
     return "mx_conv3x3v_" if w % 16 == 0 else "mx_conv3x3_"
@@ -44,6 +44,8 @@ pytestmark = pytest.mark.gpu
     (24, 40, 9, 16),     # Winograd: three chunks, a partial output block
     (32, 32, 128, 1024), # Winograd with 8 x 16-pixel blocks
     (128, 128, 20, 32),  # Winograd over 16 chunks
+    (64, 32, 13, 64),    # Winograd with 4 x 32-pixel blocks, ragged rows
+    (32, 64, 18, 48),    # Winograd with 8 x 16-pixel blocks, ragged rows
 ])
 def test_conv3x3_edges(gpu_ok, ci, co, h, w):
     from maxim_amd import plan as P
