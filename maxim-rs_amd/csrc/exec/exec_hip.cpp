@@ -2395,9 +2395,11 @@ void Gpu::build_program(const mx_plan_desc *p) {
         if (!strncmp(l.name, "mx_c3_", 6) && !aligned(dev(out), 16)) l = alt[g][0];  // so does mx_c3
         // Up to 32 outputs with a residual read: 16-wide tiles (twice the
         // waves, each with half the epilogue) measured 9% faster at the
-        // 448x640 shapes; the tile width changes no output's bits. Not for
-        // steps whose epilogue also takes a LayerNorm band (32-wide tiles).
-        if (e.r1 && sp.lno < 0 && sp.so_nband <= 0 && l.kind == 1 &&
+        // 448x640 shapes; the tile width changes no output's bits. A step whose
+        // epilogue also normalises a 32-channel LayerNorm band then holds the
+        // band in two waves of a block (44.8 -> 43.4 us for the 64 -> 32
+        // out-projections at 448x640); not for steps that leave statistics.
+        if (e.r1 && sp.so_nband <= 0 && l.kind == 1 &&
             (!strcmp(l.name, "mx_pw_ch2") || !strcmp(l.name, "mx_pw_ch2_mul"))) {
             GemmArgs a;
             memcpy(&a, l.a0, sizeof a);

@@ -645,6 +645,7 @@ MXK_PW_CT(2, 1, )
 MXK_PW_CT(2, 4, _k4)
 MXK_PW_CT(4, 1, )
 MXK_PW_CT(4, 4, _k4)
+MXK_PW_LO(1, 1, 0, )
 MXK_PW_LO(2, 1, 0, )
 MXK_PW_LO(2, 4, 0, _k4)
 MXK_PW_LO(2, 1, 1, _ln)
@@ -681,6 +682,7 @@ MXK_PW_E(mx_pw_ch2_k4_ln_f, CH, 2, 4, 1, false, false, false, 72)
 MXK_PW_E(mx_pw_ch2_k4_ln2_f, CH, 2, 4, 2, false, false, false, 72)
 MXK_PW_E(mx_pw_ch2_f_lo, CH, 2, 1, 0, false, false, true, 64)
 MXK_PW_E(mx_pw_ch2_f_lo, CH, 2, 1, 0, false, false, true, 66)
+MXK_PW_E(mx_pw_ch1_f_lo, CH, 1, 1, 0, false, false, true, 66)
 MXK_PW_E(mx_pw_ch2_k4_f_lo, CH, 2, 4, 0, false, false, true, 64)
 MXK_PW_E(mx_pw_ch2_k4_f_lo, CH, 2, 4, 0, false, false, true, 66)
 MXK_PW_E(mx_pw_ch4_k4_f_lo, CH, 4, 4, 0, false, false, true, 64)

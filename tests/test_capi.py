@@ -63,6 +63,7 @@ def test_the_code_object_is_embedded_and_complete():
     launched |= {"mx_pw_ch%d%s_mul%s" % (t, k, f) for t in (1, 2, 4) for k in ("", "_k4") for f in ("", "_f")}
     launched |= {"mx_pw_ch%d%s_t" % (t, k) for t in (1, 2, 4) for k in ("", "_k4")}
     launched |= {"mx_pw_ch%d%s%s_f_lo" % (t, k, l) for t in (2, 4) for k in ("", "_k4") for l in ("", "_ln")}
+    launched |= {"mx_pw_ch1_f_lo", "mx_pw_ch1_f_lo_e66"}
     launched |= {"mx_c3_m%d_t%d%s" % (m, t, f) for m, t in ((32, 8), (64, 4), (64, 2)) for f in ("", "_f")}
     launched |= {"mx_resize_hv%s_t%d" % (v, t) for v in ("", "4") for t in (2, 4, 8)}
     launched |= {"mx_chan%s_c%d%s" % (s, c, p) for s in ("_ln", "_ln_stats", "_scale_add_stats")
