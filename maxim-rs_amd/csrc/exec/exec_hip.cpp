@@ -1023,13 +1023,14 @@ void Gpu::init(const mx_plan_desc *p) {
             rs_need = std::max<uint64_t>(rs_need, (uint64_t)(c.c_out * r.h * r.wd));
         }
     rs_off = (so_base + pg.so_len + 63) & ~(uint64_t)63;
-    // then the partial outputs of split-reduction 4x4 convs (one op at a time)
+    // and, in the same region (a step uses one or the other, never both), the
+    // partial outputs of split-reduction 4x4 convs (one op at a time)
     uint64_t cs_need = 0;
     for (uint64_t i = 0; i < p->n_ops; ++i)
         if (p->ops[i].kind == MX_OP_CONV4X4S2 && ccfg[i].nsplit > 1)
             cs_need = std::max<uint64_t>(cs_need, (uint64_t)(ccfg[i].nsplit * p->ops[i].c_out * p->ops[i].oh * p->ops[i].ow));
-    cs_off = (rs_off + rs_need + 63) & ~(uint64_t)63;
-    scratch_len = std::max<uint64_t>(cs_off + cs_need, 64);
+    cs_off = rs_off;
+    scratch_len = std::max<uint64_t>(rs_off + std::max(rs_need, cs_need), 64);
     const uint64_t need = arena_len * 4 + wbytes + scratch_len * 4;
     size_t free_b = 0, total_b = 0;
     if (H.hipMemGetInfo(&free_b, &total_b) == 0 && need > free_b) {
