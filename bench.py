@@ -1,4 +1,4 @@
-"""Benchmark: MAXIM-3S forward pass on one MI355X.
+"""Benchmark: MAXIM-3S forward pass on one MI355X (configuration C4).
 
 One step = one MAXIM-3S forward pass (2885 ops) over one 600x400 RGB image
 reflect-padded to 640x448, with the image and the weights already resident

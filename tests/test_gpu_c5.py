@@ -1,4 +1,4 @@
-"""C5: MAXIM-3S at 4096x4096 (BASELINE's last configuration: a ~29 GiB arena
+"""C5: MAXIM-3S at 4096x4096 (the largest benchmark configuration: a ~29 GiB arena
 resident in HBM), checked through properties that do not need a full CPU
 pass (about five CPU minutes at this size):
 

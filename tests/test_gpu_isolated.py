@@ -1,4 +1,4 @@
-"""The isolated BASELINE configurations, each against the CPU oracle.
+"""The isolated benchmark configurations, each against the CPU oracle.
 
 C2: one multi-axis gated-MLP layer (ResidualSplitHeadMultiAxisGmlpLayer,
     src/model.rs:576-603) at c = 32, 256x256, block 16 + grid 16, x ~ N(0, 1):
@@ -94,7 +94,7 @@ def gmlp_range(plan):
 
 
 def test_c2_gmlp_layer_with_baseline_weights(gpu_ok, tmp_path):
-    """C2 as BASELINE.json names it: the split-head gMLP layer at c=32,
+    """C2 as the benchmark defines it: the split-head gMLP layer at c=32,
     256x256, x ~ N(0, 1), with every Dense and LayerNorm parameter of the
     layer ~ N(0, 0.02), written into a checkpoint file and read back through
     the safetensors loader (the variant comes from the file)."""

@@ -1,9 +1,9 @@
 """End-to-end parity of the HIP executor with the CPU oracle on whole MAXIM
-passes (BASELINE configs C1 and C4), plus the properties the reference checks
+passes (benchmark configurations C1 and C4), plus the properties the reference checks
 for its own GPU path: poison-filled arenas give the same bytes
 (src/exec_gpu.rs:313-340) and a pass is deterministic run to run.
 
-Bar (BASELINE.json north star): final image within max-abs 2e-3 and PSNR >= 50
+Bar: final image within max-abs 2e-3 and PSNR >= 50
 dB of the CPU path, compared on the UNCLAMPED output as well as the clamped one.
 """
 
