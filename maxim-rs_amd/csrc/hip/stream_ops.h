@@ -582,6 +582,11 @@ extern "C" __global__ __launch_bounds__(MXK_BLOCK) void mx_resize_v(ResizeArgs a
 // y): four adjacent columns per lane in the vertical pass, 128-bit stores.
 constexpr int RS_MAXT = 8;
 
+// A value every lane of the wave holds alike, as the wave's scalar.
+__device__ __forceinline__ float uniform(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, v)));
+}
+
 // acc / wsum when wsum > 0 (the CPU path's normalisation). Upsampling tables
 // mostly sum to exactly 1, and x / 1 is x in IEEE arithmetic, so those skip
 // the division and the result is the same to the bit.
@@ -623,6 +628,10 @@ __device__ void resize_hv(const Resize2Args &a) {
         const int n4 = (lead + xn + 3) >> 2;
         const float *src = a.x + ((int64_t)ch * a.h + jlo) * a.wd + x4;
         const int total = nr * n4;
+        // (r, c) of element q, advanced by 256 elements a step without a
+        // division: dr rows and dc columns, plus a carry
+        int r = tid / n4, c = tid - (tid / n4) * n4;
+        const int dr = 256 / n4, dc = 256 - dr * n4;
         for (int q0 = tid; q0 < total; q0 += 8 * 256) {
             float4 v[8];
             int at[8];
@@ -631,9 +640,14 @@ __device__ void resize_hv(const Resize2Args &a) {
                 const int q = q0 + u * 256;
                 at[u] = -1;
                 if (q < total) {
-                    const int r = q / n4, c = q - r * n4;
                     v[u] = ld4(src + (int64_t)r * a.wd + 4 * c);
                     at[u] = r * a.span + 4 * c;
+                }
+                r += dr;
+                c += dc;
+                if (c >= n4) {
+                    c -= n4;
+                    ++r;
                 }
             }
 #pragma unroll
@@ -643,6 +657,8 @@ __device__ void resize_hv(const Resize2Args &a) {
     } else {
         const float *src = a.x + ((int64_t)ch * a.h + jlo) * a.wd + xlo;
         const int total = nr * xn;
+        int r = tid / xn, c = tid - (tid / xn) * xn;
+        const int dr = 256 / xn, dc = 256 - dr * xn;
         for (int q0 = tid; q0 < total; q0 += 8 * 256) {
             float v[8];
             int at[8];
@@ -651,9 +667,14 @@ __device__ void resize_hv(const Resize2Args &a) {
                 const int q = q0 + u * 256;
                 at[u] = -1;
                 if (q < total) {
-                    const int r = q / xn, c = q - r * xn;
                     v[u] = src[(int64_t)r * a.wd + c];
                     at[u] = r * a.span + c;
+                }
+                r += dr;
+                c += dc;
+                if (c >= xn) {
+                    c -= xn;
+                    ++r;
                 }
             }
 #pragma unroll
@@ -674,14 +695,22 @@ __device__ void resize_hv(const Resize2Args &a) {
 #pragma unroll
         for (int k = 0; k < MT; ++k) w[k] = k < a.mth ? e[3 + k] : 0.0f;
         const int r0 = TW == 256 ? 0 : wave, dr = TW == 256 ? 1 : 4;
-        for (int r = r0; r < nr; r += dr) {
-            const float *sr = in + r * a.span + lead + b;
-            float acc = 0.0f;
+        // rs_norm's test once per column: columns whose taps sum to 1 (most
+        // of an upsampling) run the loop without the division
+        auto hrows = [&](auto norm) {
+            for (int r = r0; r < nr; r += dr) {
+                const float *sr = in + r * a.span + lead + b;
+                float acc = 0.0f;
 #pragma unroll
-            for (int k = 0; k < MT; ++k)
-                if (k < nt) acc += w[k] * sr[k];
-            tmp[r * TW + col] = rs_norm(acc, ws);
-        }
+                for (int k = 0; k < MT; ++k)
+                    if (k < nt) acc += w[k] * sr[k];
+                tmp[r * TW + col] = norm(acc);
+            }
+        };
+        if (ws > 0.0f && ws != 1.0f)
+            hrows([&](float acc) { return acc / ws; });
+        else
+            hrows([](float acc) { return acc; });
     }
     __syncthreads();
 
@@ -691,14 +720,16 @@ __device__ void resize_hv(const Resize2Args &a) {
         const int c0 = 4 * lane;
         if (c0 >= ncol) return;
         for (int r = wave; r < nrow; r += 4) {
+            // (row r's table entry is the wave's own: scalar registers)
             const float *e = vt + r * sv;
-            const int b = (int)e[0] - jlo, n = (int)e[1];
-            const float vs = e[2];
+            const int b = __builtin_amdgcn_readfirstlane((int)e[0]) - jlo;
+            const int n = __builtin_amdgcn_readfirstlane((int)e[1]);
+            const float vs = uniform(e[2]);
             float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
             for (int k = 0; k < MT; ++k)
                 if (k < n) {
-                    const float wk = e[3 + k];
+                    const float wk = uniform(e[3 + k]);
                     const float4 t = ld4(tmp + (b + k) * TW + c0);
                     acc[0] += wk * t.x;
                     acc[1] += wk * t.y;
@@ -706,8 +737,13 @@ __device__ void resize_hv(const Resize2Args &a) {
                     acc[3] += wk * t.w;
                 }
             float o[4];
+            if (vs > 0.0f && vs != 1.0f) {
 #pragma unroll
-            for (int u = 0; u < 4; ++u) o[u] = rs_norm(acc[u], vs);
+                for (int u = 0; u < 4; ++u) o[u] = acc[u] / vs;
+            } else {
+#pragma unroll
+                for (int u = 0; u < 4; ++u) o[u] = acc[u];
+            }
             float *yo = yrow + (int64_t)r * a.ow + c0;
             if (c0 + 3 < ncol) {
                 st4(yo, make_float4(o[0], o[1], o[2], o[3]));
@@ -721,14 +757,15 @@ __device__ void resize_hv(const Resize2Args &a) {
         if (lane >= ncol) return;
         for (int r = wave; r < nrow; r += 4) {
             const float *e = vt + r * sv;
-            const int b = (int)e[0] - jlo, n = (int)e[1];
-            const float vs = e[2];
+            const int b = __builtin_amdgcn_readfirstlane((int)e[0]) - jlo;
+            const int n = __builtin_amdgcn_readfirstlane((int)e[1]);
+            const float vs = uniform(e[2]);
             const float *t = tmp + b * TW + lane;
             float acc = 0.0f;
 #pragma unroll
             for (int k = 0; k < MT; ++k)
-                if (k < n) acc += e[3 + k] * t[k * TW];
-            yrow[(int64_t)r * a.ow + lane] = rs_norm(acc, vs);
+                if (k < n) acc += uniform(e[3 + k]) * t[k * TW];
+            yrow[(int64_t)r * a.ow + lane] = vs > 0.0f && vs != 1.0f ? acc / vs : acc;
         }
     }
 }
