@@ -46,6 +46,7 @@ pytestmark = pytest.mark.gpu
     (128, 128, 20, 32),  # Winograd over 16 chunks
     (64, 32, 13, 64),    # Winograd with 4 x 32-pixel blocks, ragged rows
     (32, 64, 18, 48),    # Winograd with 8 x 16-pixel blocks, ragged rows
+    (8, 40, 20, 96),     # Winograd, one chunk, a partial second channel block
 ])
 def test_conv3x3_edges(gpu_ok, ci, co, h, w):
     from maxim_amd import plan as P
