@@ -14,9 +14,9 @@
 //
 // A block owns 32 output channels x a TR x TC grid of tiles (2TR x 2TC output
 // pixels: 8 x 8, 8 x 16 or 4 x 32) and walks the input channels in chunks of
-// 8. Per chunk the input halo ((2TR + 2) x (2TC + 2) per channel) is staged in LDS (128-bit loads of the
-// tile's columns, the two edge columns as scalars; two buffers, so one block
-// barrier per chunk). Wave w owns the transform row xi = w (positions
+// 8. Per chunk the input halo ((2TR + 2) x (2TC + 2) per channel) is staged
+// in LDS (128-bit loads of the tile's columns stored as words, the two edge
+// columns as scalars; two buffers, so one block barrier per chunk). Wave w owns the transform row xi = w (positions
 // p = 4w + nu, nu = 0..3), and each of its lanes transforms exactly the
 // patches whose V its MFMA B operand needs - channel 4 ks + (lane / 16) of
 // tile 16 ni + (lane % 16) - for that row only (B^T d needs two rows of the
@@ -50,7 +50,10 @@ __device__ void body(const ConvArgs &a) {
     constexpr int NQT = (NQ + 255) / 256;
     constexpr int NE = CK * HH * 2;         // halo edge columns per chunk
     constexpr int NI = NT / 16;             // MFMA column tiles (tiles of 16)
-    constexpr int HALO = CK * HH * HP;
+    // channel pitch odd: the four channels of a wave's patch reads (tiles 2
+    // columns apart) fall on both bank parities
+    constexpr int CS = HH * HP + 1;
+    constexpr int HALO = CK * CS;
     constexpr int MS = 4 * 2 * BM * MP;
     constexpr int POOL = 2 * HALO > MS ? 2 * HALO : MS;
     static_assert(TC == 16 || TC == 8 || TC == 4, "2 x 16, 4 x 8 or 4 x 4 tiles");
@@ -88,13 +91,13 @@ __device__ void body(const ConvArgs &a) {
         const int q = tid + i * 256, c = q / (HH * (OW / 4)), r = (q / (OW / 4)) % HH, k = q % (OW / 4);
         const int iy = oy0 - 1 + r;
         qoff[i] = (q < NQ && iy >= 0 && iy < a.h) ? c * plane + iy * a.wd + ox0 + 4 * k : -1;
-        qlds[i] = q < NQ ? (c * HH + r) * HP + 4 + 4 * k : -1;
+        qlds[i] = q < NQ ? c * CS + r * HP + 4 + 4 * k : -1;
     }
     if (tid < NE) {
         const int c = tid / (HH * 2), r = (tid / 2) % HH, side = tid % 2, iy = oy0 - 1 + r;
         const int ix = side ? ox0 + OW : ox0 - 1;
         eoff = (iy >= 0 && iy < a.h && ix >= 0 && ix < a.wd) ? c * plane + iy * a.wd + ix : -1;
-        elds = (c * HH + r) * HP + (side ? OW + 4 : 3);
+        elds = c * CS + r * HP + (side ? OW + 4 : 3);
     }
     float4 qr[NQT], ur[4];
     float er = 0.0f;
@@ -126,7 +129,7 @@ __device__ void body(const ConvArgs &a) {
 #pragma unroll
         for (int ni = 0; ni < NI; ++ni) {
             const int c = 4 * ks + lk, t = 16 * ni + lr;
-            pofs[ks][ni] = c * HH * HP + (t / TC) * 2 * HP + (t % TC) * 2 + 3;
+            pofs[ks][ni] = c * CS + (t / TC) * 2 * HP + (t % TC) * 2 + 3;
         }
 
     f32x4 acc[4][2][NI];  // set by the first chunk
@@ -140,7 +143,13 @@ __device__ void body(const ConvArgs &a) {
         // the previous chunk's barrier)
 #pragma unroll
         for (int i = 0; i < NQT; ++i)
-            if (qlds[i] >= 0) st4(Hs + qlds[i], qr[i]);
+            if (qlds[i] >= 0) {
+                float *d = Hs + qlds[i];  // 4-byte aligned only
+                d[0] = qr[i].x;
+                d[1] = qr[i].y;
+                d[2] = qr[i].z;
+                d[3] = qr[i].w;
+            }
         if (tid < NE) Hs[elds] = er;
         __syncthreads();
         if (chunk + 1 < nchunk) fetch_halo(chunk + 1);
