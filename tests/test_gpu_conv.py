@@ -39,6 +39,7 @@ pytestmark = pytest.mark.gpu
     (20, 40, 13, 32),    # vector halo: a partial channel chunk and a partial block
     (64, 3, 10, 64),     # three output channels: the vector-ALU kernel
     (70, 3, 13, 21),     # the same with ragged tiles and a channel count off the wave split
+    (96, 4, 9, 150),     # four outputs, 4 x 64 tiles ragged in both directions
     (30, 3, 13, 21),     # three outputs from fewer inputs: 16-channel MFMA blocks
     (16, 64, 11, 40),    # Winograd: two chunks, two output blocks, ragged rows
     (24, 40, 9, 16),     # Winograd: three chunks, a partial output block
