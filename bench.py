@@ -6,21 +6,33 @@ in HBM when the timed region starts. Prints ONE JSON line:
 
   value         images/s (whole job; one GPU), from K replays of the captured
                 graph of the fused program
-  ms_per_step   ms/image
+  ms_per_step   ms/image (K back-to-back replays over the wall clock);
+                `passes` gives the median, min and max of >= 10 replays each
+                timed by its own HIP events, `e2e` the pass with the input
+                copied in and the output copied out (PCIe included; never
+                `value`), `program_roofline` the fused program's own bound
+                (each launch's max(FLOPs / 157.3 TFLOP/s, bytes / 8 TB/s),
+                summed) and the pass's fraction of it
   roofline      the dominant kernel's achieved rate against its bound (fp32
                 MFMA 157.3 TFLOP/s or HBM 8 TB/s): algorithmic FLOPs or bytes
                 per launch over the average launch duration, from the HIP
                 start/stop events each dispatch records on the executor's
                 stream over K further (eager) passes; `traffic` = its measured
-                HBM-side bytes per launch (profiles/hbm_traffic_c4.md)
+                HBM-side bytes per launch (profiles/hbm_traffic_c4.md);
+                `frac_of_own_bound` the same launches against each one's own
+                roofline min(P, AI x B)
   cpu_baseline  the CPU path (oracle/, a C restatement of the reference's
                 src/exec_cpu.rs) timed on this host: the median of three full
                 C4 passes on every host core the process may use, plus one
-                single-thread MAXIM-2S 256x256 (C1) pass for scaling
+                single-thread MAXIM-2S 256x256 (C1) pass and a single-thread
+                C2 layer (one split-head gMLP layer, c = 32, 256x256) for
+                scaling
   c5            the 4096x4096 configuration (C5, a 28.7 GiB arena): ms/image
                 over graph replays, the dominant kernel's rate there (its
                 tensors are far larger than the 256 MB Infinity Cache, so the
-                HBM figure is cache-free) and the whole pass's effective rate
+                HBM figure is cache-free), the whole pass's effective rate
+                and a per-kernel table (the memory-bound kernels and the
+                GEMMs with the most time: rate and fraction of its peak)
   validation    the last timed replay's output against the first (eager)
                 pass, bit for bit, and against the CPU path (max-abs, PSNR);
                 the run fails if they disagree
@@ -127,6 +139,25 @@ def main():
     out_last = gpu.read_buf(plan.output).reshape(out.shape)
     same = bool(np.array_equal(out_last.view(np.uint32), out.view(np.uint32)))
 
+    # Per-pass device times: >= 10 replays, each bracketed by its own events.
+    passes = None
+    if not args.eager:
+        pm = gpu.time_graph(max(10, args.steps))
+        passes = {"median_ms": float(np.median(pm)), "min_ms": float(pm.min()), "max_ms": float(pm.max()),
+                  "n": int(pm.size), "timing": "HIP events around each graph replay"}
+    # End to end: host image in, pass, host image out (PCIe included).
+    gpu.set_graph(not args.eager)
+    e2e = []
+    for _ in range(5):
+        t0 = time.perf_counter()
+        o2 = gpu.run(pad.img)
+        e2e.append(time.perf_counter() - t0)
+    gpu.set_graph(False)
+    same = same and bool(np.array_equal(o2.view(np.uint32), out.view(np.uint32)))
+    e2e_rec = {"first_pass_ms": e2e_first * 1e3, "median_ms": float(np.median(e2e)) * 1e3, "n": len(e2e),
+               "what": "mxh_run: input H2D + the pass (%s) + output D2H, host wall clock"
+                       % ("graph replay" if not args.eager else "eager launches")}
+
     # Attribution: K more passes of the same program launched eagerly, each
     # launch timed by the start/stop events its dispatch records on the
     # executor's stream. Each launch is charged its kernel's algorithmic cost
@@ -134,7 +165,7 @@ def main():
     steps = gpu.steps()
     launches = gpu.launches()
     cost = launch_costs(plan, steps, launches, R, gpu.launch_spans())
-    per_kernel = collections.defaultdict(lambda: [0.0, 0, 0.0, 0.0])  # ms, launches, flops, bytes
+    per_kernel = collections.defaultdict(lambda: [0.0, 0, 0.0, 0.0, 0.0])  # ms, launches, flops, bytes, bound ms
     ev_tot = []
     for _ in range(args.steps):
         _, tot = gpu.run_timed()
@@ -147,11 +178,13 @@ def main():
             e[1] += 1
             e[2] += f
             e[3] += by
+            e[4] += launch_bound_ms(f, by, R)
     ev_ms = float(np.median(ev_tot))
+    prog_bound_ms = sum(launch_bound_ms(f, by, R) for f, by in cost)
 
     # The dominant kernel by device time; its arithmetic intensity picks the
     # roofline axis.
-    kern, (tms, nl, fl, by) = max(per_kernel.items(), key=lambda kv: kv[1][0])
+    kern, (tms, nl, fl, by, _) = max(per_kernel.items(), key=lambda kv: kv[1][0])
     avg_s = tms / nl / 1e3
     ai = fl / by if by else 0.0
     if ai >= R.RIDGE:
@@ -164,13 +197,20 @@ def main():
     roof["avg_launch_us"] = avg_s * 1e6
     roof["launches_per_step"] = nl // args.steps
     roof["algorithmic_per_launch"] = {"gflop": fl / nl / 1e9, "mb": by / nl / 1e6}
+    roof["frac_of_own_bound"] = per_kernel[kern][4] / tms
 
     fl_all, by_all, bound_s = R.plan_cost(plan)
     print("bench: %.3f ms/image (%s), %.3f ms event-timed eager pass, %d steps for %d ops; "
           "roofline sum of per-op bounds %.2f ms" % (ms_per_step, "eager launches" if args.eager else "graph replays",
                                                       ev_ms, len(steps), n_ops, bound_s * 1e3),
           file=sys.stderr)
-    print("bench: first pass incl. H2D/D2H and launch setup %.1f ms" % (e2e_first * 1e3), file=sys.stderr)
+    print("bench: first pass incl. H2D/D2H and launch setup %.1f ms; with H2D/D2H median of %d: %.1f ms"
+          % (e2e_first * 1e3, len(e2e), e2e_rec["median_ms"]), file=sys.stderr)
+    if passes:
+        print("bench: per-pass events: median %.3f ms (min %.3f, max %.3f, %d passes)"
+              % (passes["median_ms"], passes["min_ms"], passes["max_ms"], passes["n"]), file=sys.stderr)
+    print("bench: fused program's roofline bound %.2f ms over %d launches: the pass runs at %.2f of it"
+          % (prog_bound_ms, len(launches), prog_bound_ms / ms_per_step), file=sys.stderr)
     fams = collections.defaultdict(lambda: [0.0, 0])
     for k, v in per_kernel.items():
         fams[family(k)][0] += v[0]
@@ -178,12 +218,13 @@ def main():
     tot = sum(v[0] for v in per_kernel.values())
     print("  by family: " + ", ".join("%s %.1f%%" % (k, 100 * v[0] / tot)
                                       for k, v in sorted(fams.items(), key=lambda kv: -kv[1][0])), file=sys.stderr)
-    for k, (t, n, f, b) in sorted(per_kernel.items(), key=lambda kv: -kv[1][0])[:24]:
+    for k, (t, n, f, b, _) in sorted(per_kernel.items(), key=lambda kv: -kv[1][0])[:24]:
         avg = t / n / 1e3
         print("  %-26s %5.1f%%  %4d launches/step  avg %7.1f us  %7.2f TFLOP/s  %7.1f GB/s"
               % (k, 100 * t / tot, n // args.steps, avg * 1e6, f / n / avg / 1e12, b / n / avg / 1e9),
               file=sys.stderr)
 
+    dev_arena = gpu.arena_bytes
     cus, clk = gpu.device_info()
     device = {"name": gpu.device_name, "arch": "gfx950", "cus": cus, "clock_mhz": clk // 1000}
     validation = {"replay_equals_first_pass": same}
@@ -211,9 +252,17 @@ def main():
         "dtype": "fp32",
         "data": "synthetic: seeded He-normal x0.3 weights, 600x400 smooth pattern + N(0,0.1) image",
         "config": {"workload": "C4: MAXIM-3S, 600x400 RGB reflect-padded to 640x448, one image per step",
-                   "variant": "S-3", "ops": n_ops, "launch": "eager" if args.eager else "graph", "arena_mib": round(plan.arena_bytes / 2**20, 1),
+                   "variant": "S-3", "ops": n_ops, "launch": "eager" if args.eager else "graph",
+                   "arena_mib": round(plan.arena_bytes / 2**20, 1),
+                   "device_arena_mib": round(dev_arena / 2**20, 1),
                    "gflop_per_image": round(fl_all / 1e9, 1), "gb_per_image": round(by_all / 1e9, 2),
                    "sum_of_op_bounds_ms": round(bound_s * 1e3, 2)},
+        "passes": passes,
+        "e2e": e2e_rec,
+        "program_roofline": {"bound_ms": prog_bound_ms, "kernel_ms": ev_ms, "launches": len(launches),
+                             "frac": prog_bound_ms / ms_per_step,
+                             "what": "sum over the fused program's launches of max(FLOPs / 157.3 TFLOP/s, "
+                                     "bytes / 8 TB/s), algorithmic accounting; frac = bound / ms_per_step"},
         "roofline": roof,
         "cpu_baseline": cpu,
         "device": device,
@@ -251,7 +300,8 @@ def c5_leg(w, R, steps=3):
     """C5: MAXIM-3S on a 4096x4096 image (uniform [0, 1) plus N(0, 0.05),
     clipped), the same weights: ms/image over graph replays, the dominant
     kernel's rate (its tensors are far larger than the Infinity Cache, so its
-    HBM figure is cache-free) and the whole pass's effective rate."""
+    HBM figure is cache-free), the whole pass's effective rate, the fused
+    program's roofline bound and a per-kernel table."""
     from maxim_amd import plan as P
     from maxim_amd import hip as H
     rng = np.random.default_rng(5)
@@ -273,34 +323,68 @@ def c5_leg(w, R, steps=3):
         cost = launch_costs(plan, gpu.steps(), launches, R, gpu.launch_spans())
         _, tot = gpu.run_timed()
         lt = gpu.launch_timeline()
-        per = collections.defaultdict(lambda: [0.0, 0, 0.0, 0.0])
+        per = collections.defaultdict(lambda: [0.0, 0, 0.0, 0.0, 0.0])
         for k, (st, kn) in enumerate(launches):
             e = per[kn]
             e[0] += float(lt[k])
             e[1] += 1
             e[2] += cost[k][0]
             e[3] += cost[k][1]
-        kern, (tms, nl, fl, by) = max(per.items(), key=lambda kv: kv[1][0])
+            e[4] += launch_bound_ms(cost[k][0], cost[k][1], R)
+        kern, (tms, nl, fl, by, bd) = max(per.items(), key=lambda kv: kv[1][0])
         avg_s = tms / nl / 1e3
         fl_all = sum(c[0] for c in cost)
         by_all = sum(c[1] for c in cost)
-        if fl / by >= R.RIDGE:
-            dom = {"bound": "mfma", "achieved": fl / nl / avg_s / 1e12, "peak": 157.3, "unit": "TFLOP/s"}
-        else:
-            dom = {"bound": "hbm", "achieved": by / nl / avg_s / 1e9, "peak": 8000.0, "unit": "GB/s"}
-        dom["frac"] = dom["achieved"] / dom["peak"]
+        dom = rate(fl, by, nl, avg_s, R)
         dom.update({"kernel": kern, "avg_launch_us": avg_s * 1e6, "launches_per_step": nl,
-                    "share_of_pass": tms / tot})
+                    "share_of_pass": tms / tot, "frac_of_own_bound": bd / tms})
+        # Per kernel: every memory-bound kernel (below the ridge) and the eight
+        # GEMM-shaped kernels with the most time, each against its own peak.
+        rows = []
+        for k, (t, n, f, b, _) in sorted(per.items(), key=lambda kv: -kv[1][0]):
+            if n == 0 or t <= 0 or b <= 0:
+                continue
+            r = rate(f, b, n, t / n / 1e3, R)
+            r.update({"kernel": k, "launches": n, "avg_us": 1e3 * t / n, "share": t / tot})
+            rows.append(r)
+        mem = [r for r in rows if r["bound"] == "hbm"]
+        gemm = [r for r in rows if r["bound"] == "mfma"][:8]
+        bound_ms = sum(launch_bound_ms(c[0], c[1], R) for c in cost)
         res = {"workload": "C5: MAXIM-3S, 4096x4096 RGB, one image per step", "ms_per_image": ms,
                "images_per_s": 1e3 / ms, "steps": steps, "arena_gib": round(plan.arena_bytes / 2**30, 2),
                "kernel_ms_per_pass": tot, "tflops_effective": fl_all / (ms * 1e-3) / 1e12,
                "tb_per_s_effective": by_all / (ms * 1e-3) / 1e12,
-               "algorithmic_per_pass": {"gflop": fl_all / 1e9, "gb": by_all / 1e9}, "dominant": dom}
+               "algorithmic_per_pass": {"gflop": fl_all / 1e9, "gb": by_all / 1e9}, "dominant": dom,
+               "program_roofline": {"bound_ms": bound_ms, "frac": bound_ms / ms},
+               "kernels": {"memory_bound": [compact(r) for r in mem], "gemm_top8": [compact(r) for r in gemm]}}
+        print("bench: C5 per kernel (cache-free: every level-0 tensor is 2 GB):", file=sys.stderr)
+        for r in mem + gemm:
+            print("  %-30s %4d launches  avg %8.1f us  %8.1f %-7s  %.2f of peak  %4.1f%% of the pass"
+                  % (r["kernel"], r["launches"], r["avg_us"], r["achieved"], r["unit"], r["frac"],
+                     100 * r["share"]), file=sys.stderr)
         print("bench: C5 %.1f ms/image; dominant %s %.1f us x %d (%.1f%% of %s peak)"
               % (ms, kern, avg_s * 1e6, nl, 100 * dom["frac"], dom["unit"]), file=sys.stderr, flush=True)
         return res
     finally:
         gpu.close()
+
+
+def rate(flops, nbytes, n, avg_s, R):
+    """A kernel's achieved rate over n launches of avg_s seconds against the
+    peak its arithmetic intensity puts it under (fp32 MFMA above the ridge,
+    HBM below)."""
+    if nbytes and flops / nbytes >= R.RIDGE:
+        r = {"bound": "mfma", "achieved": flops / n / avg_s / 1e12, "peak": 157.3, "unit": "TFLOP/s"}
+    else:
+        r = {"bound": "hbm", "achieved": nbytes / n / avg_s / 1e9, "peak": 8000.0, "unit": "GB/s"}
+    r["frac"] = r["achieved"] / r["peak"]
+    return r
+
+
+def compact(r):
+    return {"kernel": r["kernel"], "launches": r["launches"], "avg_us": round(r["avg_us"], 2),
+            "bound": r["bound"], "achieved": round(r["achieved"], 2), "unit": r["unit"],
+            "frac": round(r["frac"], 3), "share": round(r["share"], 4)}
 
 
 TRAFFIC = os.path.join(ROOT, "profiles", "hbm_traffic_c4.md")
@@ -454,15 +538,46 @@ def cpu_baseline(plan, img, threads):
     w2 = P.Weights.synthetic("S-2", seed=SEED, gain=GAIN, bias_std=0.02, ln_std=0.1)
     c1 = P.Plan(w2, 256, 256)
     dt1, _ = one(c1, np.random.default_rng(2).random((3, 256, 256), dtype=np.float32), 1)
-    print("bench: CPU C4 %s s on %d threads, C1 %.1f s on 1 thread (%s)"
-          % (", ".join("%.2f" % t for t in times), used, dt1, cpu_model()), file=sys.stderr, flush=True)
+    # C2: the first split-head gMLP layer of the MAXIM-2S 256x256 plan (its 25
+    # ops, LayerNorm_in through the residual add), x ~ N(0, 1), one thread
+    c2 = P.Plan(w2, 256, 256, named=True, deep=True)
+    first, last, x = gmlp_layer_range(c2)
+    arena = np.zeros(c2.arena_len, np.float32)
+    arena[int(c2.offs[x]):int(c2.offs[x]) + c2.buf_len(x)] = \
+        np.random.default_rng(8).standard_normal(c2.buf_len(x)).astype(np.float32)
+    t0 = time.perf_counter()
+    O.run_range(c2, arena, first, last, 1)
+    dt2 = time.perf_counter() - t0
+    print("bench: CPU C4 %s s on %d threads, C1 %.1f s and C2 %.2f s on 1 thread (%s)"
+          % (", ".join("%.2f" % t for t in times), used, dt1, dt2, cpu_model()), file=sys.stderr, flush=True)
     rec = {"value": 1.0 / med, "unit": "images/s", "cores": used, "kind": "port",
            "sample": "median of 3 full MAXIM-3S 640x448 passes (2885 ops) of the C restatement of "
                      "src/exec_cpu.rs: %s s" % ", ".join("%.2f" % t for t in times),
            "cpu_model": cpu_model(), "host_cores_visible": os.cpu_count(),
            "c1_single_thread": {"seconds": dt1, "images_per_s": 1.0 / dt1,
-                                "workload": "C1: MAXIM-2S 256x256, one pass, 1 thread"}}
+                                "workload": "C1: MAXIM-2S 256x256, one pass, 1 thread"},
+           "c2_single_thread": {"seconds": dt2, "ops": last - first,
+                                "workload": "C2: one split-head gMLP layer (c=32, 256x256, block 16 + grid 16), "
+                                            "1 thread"}}
     return rec, ref
+
+
+def gmlp_layer_range(plan):
+    """(first, last, x): the ops of the first split-head gMLP layer of a
+    `named` MAXIM plan - after the first encoder block's Conv_0 (buffer x)
+    through the layer's residual add."""
+    d = dict(plan.dumps)
+    x = d["stage_0_encoder_block_0_mid_conv"]
+    y = d["stage_0_encoder_block_0_mid_g0_gmlp"]
+    first = next(i for i, op in enumerate(plan.ops) if op.dst == x) + 1
+    last = next(i for i, op in enumerate(plan.ops) if op.dst == y) + 1
+    return first, last, x
+
+
+def launch_bound_ms(flops, nbytes, R):
+    """A launch's roofline time: the larger of its FLOPs at the fp32 MFMA peak
+    and its bytes at the HBM peak (ms)."""
+    return 1e3 * max(flops / R.PEAK_FP32_MFMA, nbytes / R.PEAK_HBM)
 
 
 if __name__ == "__main__":

@@ -56,13 +56,19 @@ int mxh_step_op(mxh_gpu *g, const mx_plan_desc *plan, uint64_t i);
  * the pass, and the kernels' scratch (channel-mean partial sums, LayerNorm
  * statistics) is the code object's static array of 32 MiB per device, in
  * place of the per-executor scratch mxh_run uses. A plan whose scratch needs
- * more (e.g. 4096x4096) is refused with the numbers. Asynchronous on the
- * executor's stream (mxh_sync waits). Every call on a device shares that
- * device's array: calls that overlap on one device (executors run on their
- * own streams) race, so let one finish before another starts. Every pass
- * writes the scratch before reading it, so nothing needs clearing. */
+ * more (e.g. 4096x4096) is refused with the numbers. Asynchronous, in stream
+ * order on `stream` (a hipStream_t; NULL: the executor's own stream, which
+ * mxh_sync waits for): the input copy, every kernel and the output copy are
+ * queued there after whatever the caller queued before, so d_input must be
+ * complete by then in that stream's order, d_output holds the result once
+ * the stream has passed the call, and a caller capturing `stream` into a HIP
+ * graph captures the whole pass (two device-to-device copies and kernel
+ * nodes; no memsets). Every call on a device shares that device's array:
+ * calls that overlap on one device (on different streams, or executors on
+ * their own streams) race, so let one finish before another starts. Every
+ * pass writes the scratch before reading it, so nothing needs clearing. */
 int mxh_run_noalloc(mxh_gpu *g, const mx_plan_desc *plan, const float *d_input, uint64_t n_in, float *d_output,
-                    uint64_t n_out);
+                    uint64_t n_out, void *stream);
 /* Every op over the image already in the arena as ONE captured HIP graph
  * (captured on the first call, replayed after), asynchronously. The graph
  * launches exactly the kernels mxh_run_ops would, in the same order. */
@@ -145,6 +151,13 @@ int mxh_launch_timeline(mxh_gpu *g, float *ms, uint64_t n);
  * the executor's stream; `ms` gets the total device time. */
 int mxh_time_ops(mxh_gpu *g, const mx_plan_desc *plan, uint64_t first, uint64_t last, int iters,
                  float *ms);
+
+/* `n` passes over the image already in the arena, each one replay of the
+ * captured graph (mxh_run_graph) bracketed by its own pair of HIP events on
+ * the executor's stream, back to back, one synchronisation at the end;
+ * ms[k] gets pass k's device milliseconds. No counterpart in the reference:
+ * the per-pass times a median is taken over. */
+int mxh_time_graph(mxh_gpu *g, const mx_plan_desc *plan, int n, float *ms);
 
 /* Gpu::device_name / arena_bytes / weight_bytes / pool_bytes / ops_launched
  * (src/exec_gpu.rs:165-183). kernels_launched counts launches (one op may be

@@ -201,10 +201,20 @@ int mx_preprocess(const float *img, int64_t c, int64_t h, int64_t w, int64_t fac
 int mx_crop_out(const float *img, int64_t c, int64_t ph, int64_t pw, int64_t even_h,
                 int64_t even_w, int64_t orig_h, int64_t orig_w, float *out);
 
-/* image::read_png (src/image.rs:33-72): an 8-bit grayscale, gray + alpha, RGB
- * or RGBA PNG as [3][h][w] floats in 0..1 (gray expanded, alpha dropped).
- * Two calls: with out == NULL it reports h and w; then with 3*h*w floats. */
-int mx_png_read(const char *path, float *out, int64_t *h, int64_t *w);
+/* image::read_png / read_png_stream (src/image.rs:33-72): an 8-bit grayscale,
+ * gray + alpha, RGB or RGBA PNG, plain or Adam7-interlaced, decoded once
+ * into a handle: from the file `path`, or, with path NULL, from the n bytes
+ * at data (the CLI's `-i -`, src/main.rs:205-214). Reports h and w. */
+typedef struct mx_png mx_png;
+int mx_png_open(const char *path, const unsigned char *data, size_t n, mx_png **img, int64_t *h, int64_t *w);
+/* The decoded image as [3][h][w] floats in 0..1 (gray expanded, alpha
+ * dropped) into out, which holds cap floats; refused when cap < 3*h*w. */
+int mx_png_pixels(const mx_png *img, float *out, size_t cap);
+void mx_png_close(mx_png *img);
+/* image::write_png_stream (src/image.rs:84-104) into memory (the CLI's
+ * `-o -`, src/main.rs:439-448): sets *n to the PNG's size; with out != NULL
+ * also writes the bytes, refused when cap < *n. */
+int mx_png_encode(const float *img, int64_t h, int64_t w, unsigned char *out, size_t cap, size_t *n);
 /* image::write_png (src/image.rs:74-104): [3][h][w] in 0..1 as an 8-bit RGB
  * PNG, each value clamped and rounded half up. */
 int mx_png_write(const char *path, const float *img, int64_t h, int64_t w);

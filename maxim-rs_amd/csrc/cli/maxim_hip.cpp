@@ -3,10 +3,13 @@
 //
 //   maxim_hip -m MODEL.safetensors [-i IN.png] [-o OUT.png] [-q]
 //
-// reads the PNG, runs mxh_enhance (checkpoint -> padded plan -> device pass
-// -> crop) and writes the PNG. As in the reference, a pass that fails is
-// reported, not retried elsewhere; there is no CPU backend in this binary.
+// reads the PNG (from stdin when -i is `-` or absent, src/main.rs:205-214),
+// runs mxh_enhance (checkpoint -> padded plan -> device pass -> crop) and
+// writes the PNG (to stdout when -o is `-` or absent, src/main.rs:439-448).
+// As in the reference, a pass that fails is reported, not retried elsewhere;
+// there is no CPU backend in this binary.
 
+#include <cerrno>
 #include <chrono>
 #include <cstdio>
 #include <cstring>
@@ -16,12 +19,22 @@
 #include "maxim_hip.h"
 
 static int usage() {
-    std::fprintf(stderr, "usage: maxim_hip -m MODEL.safetensors -i IN.png -o OUT.png [-q]\n");
+    std::fprintf(stderr,
+                 "usage: maxim_hip -m MODEL.safetensors [-i IN.png] [-o OUT.png] [-q]\n"
+                 "    -m, --model <path>    converted .safetensors checkpoint\n"
+                 "    -i, --input <path>    input PNG, or - for stdin (default: stdin)\n"
+                 "    -o, --output <path>   output PNG, or - for stdout (default: stdout)\n"
+                 "    -q, --quiet           no progress output\n");
     return 2;
 }
 
+static int fail() {
+    std::fprintf(stderr, "maxim: %s\n", mx_last_error());
+    return 1;
+}
+
 int main(int argc, char **argv) {
-    std::string model, in, out;
+    std::string model, in = "-", out = "-";
     bool quiet = false;
     for (int i = 1; i < argc; ++i) {
         const std::string a = argv[i];
@@ -39,31 +52,47 @@ int main(int argc, char **argv) {
         }
         return usage();
     }
-    if (model.empty() || in.empty() || out.empty()) return usage();
+    if (model.empty()) return usage();
     if (mxh_driver_ready() != 0) {
         std::fprintf(stderr, "maxim: hip: %s\n", mx_last_error());
         return 1;
     }
+    // The image: decoded once, from the file or from everything on stdin.
+    mx_png *png = nullptr;
     int64_t h = 0, w = 0;
-    if (mx_png_read(in.c_str(), nullptr, &h, &w) != 0) {
-        std::fprintf(stderr, "maxim: %s\n", mx_last_error());
-        return 1;
+    if (in == "-") {
+        std::vector<unsigned char> buf;
+        unsigned char chunk[1 << 16];
+        size_t k;
+        while ((k = std::fread(chunk, 1, sizeof chunk, stdin)) > 0) buf.insert(buf.end(), chunk, chunk + k);
+        if (std::ferror(stdin)) {
+            std::fprintf(stderr, "maxim: read stdin: %s\n", std::strerror(errno));
+            return 1;
+        }
+        if (mx_png_open(nullptr, buf.data(), buf.size(), &png, &h, &w) != 0) return fail();
+    } else if (mx_png_open(in.c_str(), nullptr, 0, &png, &h, &w) != 0) {
+        return fail();
     }
     std::vector<float> img((size_t)(3 * h * w)), res(img.size());
-    if (mx_png_read(in.c_str(), img.data(), &h, &w) != 0) {
-        std::fprintf(stderr, "maxim: %s\n", mx_last_error());
-        return 1;
-    }
+    const int got = mx_png_pixels(png, img.data(), img.size());
+    mx_png_close(png);
+    if (got != 0) return fail();
     const auto t0 = std::chrono::steady_clock::now();
-    if (mxh_enhance(model.c_str(), img.data(), h, w, res.data()) != 0) {
-        std::fprintf(stderr, "maxim: %s\n", mx_last_error());
-        return 1;
-    }
+    if (mxh_enhance(model.c_str(), img.data(), h, w, res.data()) != 0) return fail();
     const double secs = std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count();
-    if (mx_png_write(out.c_str(), res.data(), h, w) != 0) {
-        std::fprintf(stderr, "maxim: %s\n", mx_last_error());
-        return 1;
+    if (!quiet) std::fprintf(stderr, "maxim: %lldx%lld enhanced in %.2fs on the GPU\n", (long long)w, (long long)h, secs);
+    if (out == "-") {
+        size_t n = 0;
+        if (mx_png_encode(res.data(), h, w, nullptr, 0, &n) != 0) return fail();
+        std::vector<unsigned char> bytes(n);
+        if (mx_png_encode(res.data(), h, w, bytes.data(), bytes.size(), &n) != 0) return fail();
+        if (std::fwrite(bytes.data(), 1, n, stdout) != n || std::fflush(stdout) != 0) {
+            std::fprintf(stderr, "maxim: stdout: %s\n", std::strerror(errno));
+            return 1;
+        }
+    } else {
+        if (mx_png_write(out.c_str(), res.data(), h, w) != 0) return fail();
+        if (!quiet) std::fprintf(stderr, "maxim: wrote %s\n", out.c_str());
     }
-    if (!quiet) std::fprintf(stderr, "maxim: %lldx%lld enhanced in %.2fs on the GPU, wrote %s\n", (long long)w, (long long)h, secs, out.c_str());
     return 0;
 }

@@ -520,9 +520,10 @@ public:
         if (p->n_ops != n_ops || p->n_bufs != n_bufs || p->arena_len != plan_arena_len)
             throw Error("this executor was built for a different plan");
     }
-    void launch(Launch &l) {
+    // on: the stream to launch on (the executor's own when null)
+    void launch(Launch &l, hipStream_t on = nullptr) {
         void *params[2] = {l.a0, l.a1};
-        check(H.hipModuleLaunchKernel(l.f, l.g[0], l.g[1], l.g[2], l.b[0], l.b[1], l.b[2], l.shm, stream,
+        check(H.hipModuleLaunchKernel(l.f, l.g[0], l.g[1], l.g[2], l.b[0], l.b[1], l.b[2], l.shm, on ? on : stream,
                                       params, nullptr),
               l.name);
         ++kernels;
@@ -3186,7 +3187,7 @@ int mxh_run(mxh_gpu *g, const mx_plan_desc *plan, const float *input, uint64_t n
 }
 
 int mxh_run_noalloc(mxh_gpu *g, const mx_plan_desc *plan, const float *d_input, uint64_t n_in, float *d_output,
-                    uint64_t n_out) {
+                    uint64_t n_out, void *stream) {
     return guard([&] {
         Gpu &x = *G(g);
         x.check_plan(plan);
@@ -3199,13 +3200,16 @@ int mxh_run_noalloc(mxh_gpu *g, const mx_plan_desc *plan, const float *d_input, 
                             " bytes of scratch; the static scratch of mxh_run_noalloc holds " +
                             std::to_string((uint64_t)MXK_NOALLOC_SCRATCH_FLOATS * 4) + " (mxh_run has no such limit)");
         auto &H = x.H;
-        mxh::check(H.hipMemcpyAsync(x.arena + x.doff[plan->input], d_input, n_in * 4, mxh::kMemcpyD2D, x.stream),
+        // the caller's stream when given (stream order with its own work;
+        // a capture of that stream records the pass), else the executor's
+        const mxh::hipStream_t on = stream ? (mxh::hipStream_t)stream : x.stream;
+        mxh::check(H.hipMemcpyAsync(x.arena + x.doff[plan->input], d_input, n_in * 4, mxh::kMemcpyD2D, on),
                    "hipMemcpyAsync(input)");
         for (mxh::Step &st : x.prog_na) {
-            for (auto &l : st.launches) x.launch(l);
+            for (auto &l : st.launches) x.launch(l, on);
             x.launched += st.last - st.first;
         }
-        mxh::check(H.hipMemcpyAsync(d_output, x.arena + x.doff[plan->output], n_out * 4, mxh::kMemcpyD2D, x.stream),
+        mxh::check(H.hipMemcpyAsync(d_output, x.arena + x.doff[plan->output], n_out * 4, mxh::kMemcpyD2D, on),
                    "hipMemcpyAsync(output)");
     });
 }
@@ -3389,6 +3393,32 @@ int mxh_timeline(mxh_gpu *g, float *per_op_ms, uint64_t n, float *total_ms) {
         if (!x.have_timeline) throw mx::Error("no timeline recorded (mxh_set_timeline, then mxh_run)");
         if (per_op_ms) memcpy(per_op_ms, x.per_op_ms.data(), sizeof(float) * std::min<uint64_t>(n, x.per_op_ms.size()));
         if (total_ms) *total_ms = x.total_ms;
+    });
+}
+
+int mxh_time_graph(mxh_gpu *g, const mx_plan_desc *plan, int n, float *ms) {
+    return guard([&] {
+        Gpu &x = *G(g);
+        x.check_plan(plan);
+        if (n <= 0 || !ms) throw mx::Error("mxh_time_graph: no passes or no output");
+        auto &H = x.H;
+        std::vector<mxh::hipEvent_t> ev(2 * (size_t)n, nullptr);
+        try {
+            for (auto &e : ev) mxh::check(H.hipEventCreate(&e), "hipEventCreate");
+            for (int k = 0; k < n; ++k) {
+                mxh::check(H.hipEventRecord(ev[2 * k], x.stream), "hipEventRecord");
+                x.run_graph();
+                mxh::check(H.hipEventRecord(ev[2 * k + 1], x.stream), "hipEventRecord");
+            }
+            x.sync();
+            for (int k = 0; k < n; ++k)
+                mxh::check(H.hipEventElapsedTime(&ms[k], ev[2 * k], ev[2 * k + 1]), "hipEventElapsedTime");
+        } catch (...) {
+            for (auto &e : ev)
+                if (e) H.hipEventDestroy(e);
+            throw;
+        }
+        for (auto &e : ev) H.hipEventDestroy(e);
     });
 }
 

@@ -109,10 +109,13 @@ def verify_walk(plan, image, cpu_step, judge=None, resync=False, tol=1e-3, max_r
 
 
 def timeline_report(plan, image, out=print):
-    """The --profile census of one pass: per-op device times (fusion off, an
-    event pair per op) by family, by shape and the slowest five; then the
-    fused program's launches by kernel. Returns (per-op ms, per-kernel
-    {kernel: [ms, launches]})."""
+    """The --profile census of one pass (src/main.rs:526-656): per-op device
+    times (fusion off, an event pair per op) by family, by shape and the
+    slowest five; then the fused program's launches by kernel (run_timed:
+    each launch timed by its own dispatch events). Returns a dict: per_op
+    (ms per op), total_ms (the timeline's total), families ({family: [ms,
+    ops]}), slowest (the five op indices), kernels ({kernel: [ms,
+    launches]}) and fused_total_ms (run_timed's total)."""
     from . import hip as H
     gpu = H.Gpu(plan)
     try:
@@ -141,12 +144,13 @@ def timeline_report(plan, image, out=print):
             if n >= 16:
                 out("  %9.2f ms %5dx  %s   (%.4f ms/op)" % (ms, n, k, ms / n))
         out("slowest ops:")
-        for i in np.argsort(-per_op)[:5]:
-            out("  op %d %.3f ms  %s" % (int(i), float(per_op[i]), plan.ops[int(i)].describe()))
+        slowest = [int(i) for i in np.argsort(-per_op, kind="stable")[:5]]
+        for i in slowest:
+            out("  op %d %.3f ms  %s" % (i, float(per_op[i]), plan.ops[i].describe()))
         # the fused program, launch by launch
         gpu.set_timeline(False)
         gpu.set_fusion(True)
-        gpu.run_timed()
+        _, fused_total = gpu.run_timed()
         kern = collections.defaultdict(lambda: [0.0, 0])
         for (st, k), ms in zip(gpu.launches(), gpu.launch_timeline()):
             kern[k][0] += float(ms)
@@ -155,7 +159,9 @@ def timeline_report(plan, image, out=print):
         out("fused program: %.2f ms of kernel time, %d launches" % (tot, sum(v[1] for v in kern.values())))
         for k, (ms, n) in sorted(kern.items(), key=lambda kv: -kv[1][0])[:12]:
             out("  %-30s %5d x %8.1f us  %5.1f%%" % (k, n, 1e3 * ms / n, 100 * ms / max(tot, 1e-9)))
-        return per_op, dict(kern)
+        return {"per_op": per_op, "total_ms": total, "families": {k: list(v) for k, v in fams.items()},
+                "slowest": slowest, "kernels": {k: list(v) for k, v in kern.items()},
+                "fused_total_ms": fused_total}
     finally:
         gpu.close()
 

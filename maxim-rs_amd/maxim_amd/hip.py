@@ -63,7 +63,8 @@ def _lib():
             "mxh_op_kernel": (C.c_char_p, [V, U]),
             "mxh_device_info": (I, [V, C.POINTER(C.c_int), C.POINTER(C.c_int)]),
             "mxh_device_memory": (I, [C.POINTER(C.c_uint64), C.POINTER(C.c_uint64)]),
-            "mxh_run_noalloc": (I, [V, D, V, U, V, U]),
+            "mxh_run_noalloc": (I, [V, D, V, U, V, U, V]),
+            "mxh_time_graph": (I, [V, D, C.c_int, V]),
             "mxh_enhance": (I, [C.c_char_p, V, C.c_int64, C.c_int64, V]),
         }
         for name, (res, args) in sig.items():
@@ -127,12 +128,14 @@ class Gpu:
         _check(_lib().mxh_run(self._h, self._d, img.ctypes.data, img.size, out.ctypes.data, out.size))
         return out
 
-    def run_noalloc(self, d_input, d_output):
+    def run_noalloc(self, d_input, d_output, stream=None):
         """mxh_run_noalloc: the pass from device pointer d_input to d_output
-        (integers), asynchronously, with no allocation (the static scratch)."""
+        (integers), asynchronously on `stream` (a hipStream_t as an integer;
+        None: the executor's stream), with no allocation (the static
+        scratch)."""
         c, h, w = self.plan.bufs[self.plan.input]
         co, ho, wo = self.plan.bufs[self.plan.output]
-        _check(_lib().mxh_run_noalloc(self._h, self._d, d_input, c * h * w, d_output, co * ho * wo))
+        _check(_lib().mxh_run_noalloc(self._h, self._d, d_input, c * h * w, d_output, co * ho * wo, stream))
 
     def begin(self, image):
         img = np.ascontiguousarray(image, dtype=np.float32)
@@ -243,6 +246,13 @@ class Gpu:
         n = _lib().mxh_launches(self._h)
         ms = np.empty(n, np.float32)
         _check(_lib().mxh_launch_timeline(self._h, ms.ctypes.data, n))
+        return ms
+
+    def time_graph(self, n):
+        """n graph replays back to back, each bracketed by its own events:
+        per-pass device ms."""
+        ms = np.empty(n, np.float32)
+        _check(_lib().mxh_time_graph(self._h, self._d, n, ms.ctypes.data))
         return ms
 
     def time_ops(self, first, last, iters=1):

@@ -114,7 +114,11 @@ def _declare(lib):
         "mx_crop_out": (C.c_int, [P, C.c_int64, C.c_int64, C.c_int64, C.c_int64, C.c_int64,
                                   C.c_int64, C.c_int64, P]),
         "mx_memguard_check": (C.c_int, [P, C.c_int, C.c_int64, C.POINTER(C.c_uint64)]),
-        "mx_png_read": (C.c_int, [C.c_char_p, P, C.POINTER(C.c_int64), C.POINTER(C.c_int64)]),
+        "mx_png_open": (C.c_int, [C.c_char_p, P, C.c_size_t, C.POINTER(C.c_void_p), C.POINTER(C.c_int64),
+                                  C.POINTER(C.c_int64)]),
+        "mx_png_pixels": (C.c_int, [C.c_void_p, P, C.c_size_t]),
+        "mx_png_close": (None, [C.c_void_p]),
+        "mx_png_encode": (C.c_int, [P, C.c_int64, C.c_int64, P, C.c_size_t, C.POINTER(C.c_size_t)]),
         "mx_png_write": (C.c_int, [C.c_char_p, P, C.c_int64, C.c_int64]),
     }
     for name, (res, args) in sig.items():
@@ -386,13 +390,33 @@ class CustomPlan:
         return self._weights[i]
 
 
-def read_png(path):
-    """image::read_png: an 8-bit PNG as a [3][h][w] float32 array in 0..1."""
-    h, w = C.c_int64(), C.c_int64()
-    _check(lib().mx_png_read(path.encode(), None, C.byref(h), C.byref(w)))
-    out = np.empty((3, h.value, w.value), np.float32)
-    _check(lib().mx_png_read(path.encode(), out.ctypes.data, C.byref(h), C.byref(w)))
+def read_png(path=None, data=None):
+    """image::read_png / read_png_stream: an 8-bit PNG (plain or Adam7
+    interlaced), from the file `path` or the bytes `data`, as a [3][h][w]
+    float32 array in 0..1; decoded once."""
+    h, w, img = C.c_int64(), C.c_int64(), C.c_void_p()
+    if path is not None:
+        _check(lib().mx_png_open(path.encode(), None, 0, C.byref(img), C.byref(h), C.byref(w)))
+    else:
+        buf = (C.c_ubyte * len(data)).from_buffer_copy(data)
+        _check(lib().mx_png_open(None, C.cast(buf, C.c_void_p), len(data), C.byref(img), C.byref(h), C.byref(w)))
+    try:
+        out = np.empty((3, h.value, w.value), np.float32)
+        _check(lib().mx_png_pixels(img, out.ctypes.data, out.size))
+    finally:
+        lib().mx_png_close(img)
     return out
+
+
+def encode_png(img):
+    """image::write_png_stream into memory: [3][h][w] in 0..1 as PNG bytes."""
+    a = np.ascontiguousarray(img, np.float32)
+    assert a.ndim == 3 and a.shape[0] == 3, a.shape
+    n = C.c_size_t()
+    _check(lib().mx_png_encode(a.ctypes.data, a.shape[1], a.shape[2], None, 0, C.byref(n)))
+    out = (C.c_ubyte * n.value)()
+    _check(lib().mx_png_encode(a.ctypes.data, a.shape[1], a.shape[2], C.cast(out, C.c_void_p), n.value, C.byref(n)))
+    return bytes(out)
 
 
 def write_png(path, img):

@@ -64,3 +64,36 @@ def test_enhance_refuses_a_bad_checkpoint(gpu_ok, tmp_path):
     open(bad, "wb").write(b"\x08\x00\x00\x00\x00\x00\x00\x00{}      ")
     with pytest.raises(P.MaximError):
         H.enhance(bad, np.zeros((3, 64, 64), np.float32))
+
+
+def test_cli_stdin_stdout_interlaced(gpu_ok, tmp_path):
+    """`maxim_hip -m CKPT` with the image on stdin and the result on stdout
+    (`-i -` / `-o -`, and the same with both options absent, as
+    src/main.rs:205-214,439-448), the input an Adam7-interlaced RGBA PNG of
+    an odd size, against the CPU path at the 8-bit bar."""
+    from maxim_amd import plan as P
+    from test_png import write_interlaced_png
+    ckpt = str(tmp_path / "maxim_s2.safetensors")
+    weights("S-2").save(ckpt)
+    img = smooth_image(70, 90, seed=9)
+    px = np.concatenate([np.rint(img * 255).astype(np.uint8).transpose(1, 2, 0),
+                         np.full((70, 90, 1), 200, np.uint8)], axis=2)
+    src = str(tmp_path / "in_a7.png")
+    write_interlaced_png(src, px, 6, 6)
+    got = P.read_png(src)
+    assert np.array_equal(got, np.rint(img * 255).astype(np.float32) / np.float32(255.0))
+    pad = P.preprocess(got, 64)
+    plan = P.Plan(P.Weights.open(ckpt), *pad.img.shape[1:])
+    arena = run_oracle(plan, pad.img)
+    o = int(plan.offs[plan.output])
+    ref = P.crop_out(arena[o:o + pad.img.size].reshape(pad.img.shape), pad)
+    want = np.rint(np.clip(ref, 0, 1) * 255)
+    exe = os.path.join(ROOT, "maxim-rs_amd", "lib", "maxim_hip")
+    data = open(src, "rb").read()
+    for args in (["-i", "-", "-o", "-"], []):
+        print("maxim_hip %s (stdin -> stdout)" % " ".join(args), flush=True)
+        r = subprocess.run([exe, "-m", ckpt, "-q"] + args, input=data, capture_output=True, timeout=300)
+        assert r.returncode == 0, r.stderr.decode()
+        out = P.read_png(data=r.stdout)
+        assert out.shape == (3, 70, 90)
+        assert np.abs(np.rint(out * 255) - want).max() <= 1.0

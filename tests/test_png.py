@@ -144,3 +144,86 @@ def test_refusals(tmp_path):
         P().read_png(path)
     with pytest.raises(P().MaximError):
         P().read_png(str(tmp_path / "missing.png"))
+
+
+# Adam7 (PNG 1.2, 8.2): pass p takes rows R0[p] + k * DR[p] and columns
+# C0[p] + k * DC[p]; each non-empty pass is filtered as an image of its own.
+R0, C0 = (0, 0, 4, 0, 2, 0, 1), (0, 4, 0, 2, 0, 1, 0)
+DR, DC = (8, 8, 8, 4, 4, 2, 2), (8, 8, 4, 4, 2, 2, 1)
+
+
+def write_interlaced_png(path, px, ctype, level, filters=(0, 1, 2, 3, 4)):
+    h, w, ch = px.shape
+    raw = b""
+    for p in range(7):
+        sub = px[R0[p]::DR[p], C0[p]::DC[p]]
+        if sub.shape[0] == 0 or sub.shape[1] == 0:
+            continue  # an empty pass contributes no bytes at all
+        sh, sw = sub.shape[:2]
+        # rotate the filter list per pass so every filter meets every pass
+        raw += filter_rows(np.ascontiguousarray(sub).reshape(sh, sw * ch), ch, filters[p % 5:] + filters[:p % 5])
+    data = b"\x89PNG\r\n\x1a\n" + chunk(b"IHDR", struct.pack(">IIBBBBB", w, h, 8, ctype, 0, 0, 1))
+    data += chunk(b"IDAT", zlib.compress(raw, level)) + chunk(b"IEND", b"")
+    open(path, "wb").write(data)
+
+
+@pytest.mark.parametrize("h,w", [(37, 53), (1, 1), (1, 9), (5, 1), (3, 3), (8, 8), (17, 16)])
+@pytest.mark.parametrize("ctype,ch", [(2, 3), (6, 4), (0, 1), (4, 2)])
+def test_read_interlaced(tmp_path, h, w, ctype, ch):
+    """Adam7 files (the reference's png crate deinterlaces them in
+    next_frame), including sizes where some of the seven passes are empty."""
+    rng = np.random.default_rng(h * 100 + w + ctype)
+    px = rng.integers(0, 256, (h, w, ch)).astype(np.uint8)
+    path = str(tmp_path / "a7.png")
+    write_interlaced_png(path, px, ctype, 6)
+    got = P().read_png(path)
+    rgb = px[..., :3] if ch >= 3 else np.repeat(px[..., :1], 3, axis=2)
+    assert np.array_equal(got, rgb.transpose(2, 0, 1).astype(np.float32) / np.float32(255.0))
+    # an independent decoder agrees on the file (Pillow deinterlaces on load)
+    from PIL import Image
+    ref = np.asarray(Image.open(path).convert("RGB"))
+    assert np.array_equal(got, ref.transpose(2, 0, 1).astype(np.float32) / np.float32(255.0))
+
+
+def test_file_from_pillow(tmp_path):
+    """A file Pillow's encoder writes (interlacing is not among its save
+    options, so this pins the plain path against a third-party encoder)."""
+    from PIL import Image
+    rng = np.random.default_rng(11)
+    px = rng.integers(0, 256, (29, 31, 3)).astype(np.uint8)
+    path = str(tmp_path / "pil.png")
+    Image.fromarray(px).save(path, optimize=True)
+    assert np.array_equal(P().read_png(path), px.transpose(2, 0, 1).astype(np.float32) / np.float32(255.0))
+
+
+def test_stream_forms(tmp_path):
+    """read_png_stream / write_png_stream (the CLI's `-i -` and `-o -`): the
+    same image from bytes as from the file, and the encoder's bytes are the
+    file's bytes."""
+    rng = np.random.default_rng(5)
+    q = rng.integers(0, 256, (3, 21, 34)).astype(np.float32) / np.float32(255.0)
+    path = str(tmp_path / "s.png")
+    P().write_png(path, q)
+    data = open(path, "rb").read()
+    assert P().encode_png(q) == data
+    assert np.array_equal(P().read_png(data=data), q)
+    with pytest.raises(P().MaximError, match="not a PNG"):
+        P().read_png(data=b"not a png at all")
+
+
+def test_pixels_refuses_a_short_buffer(tmp_path):
+    """The decoded image is copied out only into a buffer that holds it."""
+    import ctypes as C
+    q = np.zeros((3, 6, 7), np.float32)
+    path = str(tmp_path / "c.png")
+    P().write_png(path, q)
+    lib = P().lib()
+    h, w, img = C.c_int64(), C.c_int64(), C.c_void_p()
+    assert lib.mx_png_open(path.encode(), None, 0, C.byref(img), C.byref(h), C.byref(w)) == 0
+    try:
+        out = np.zeros(3 * 6 * 7, np.float32)
+        assert lib.mx_png_pixels(img, out.ctypes.data, out.size - 1) != 0
+        assert b"needs 126" in lib.mx_last_error()
+        assert lib.mx_png_pixels(img, out.ctypes.data, out.size) == 0
+    finally:
+        lib.mx_png_close(img)
