@@ -2554,7 +2554,10 @@ void Gpu::build_program(const mx_plan_desc *p) {
         l.f = fn(l.name);
         l.g[0] = (unsigned)(k4 ? tiles : (tiles + 3) / 4);
         l.g[1] = 1;
-        a.lo = LnOut{scale, bias, y, eps, (int32_t)r0, keep, G, mode, nband, 0};
+        // a group of waves of 32+ channels each sums its band per wave, then
+        // adds the partials in wave order (not the LayerNorm kernels' order:
+        // MAXIM_PLAN_ORDER=1 keeps theirs)
+        a.lo = LnOut{scale, bias, y, eps, (int32_t)r0, keep, G, mode, nband, G > 1 && tmw >= 2 && !plan_order ? 1 : 0};
         set_args(l, a);
         return true;
     };

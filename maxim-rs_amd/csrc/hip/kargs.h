@@ -194,11 +194,15 @@ struct BlockMap {
 //       the LayerNorm statistics kernels' values) written to y as
 //       [nband][2][N] at the pixel's image position (through ymap), for the
 //       GEMMs that fold those LayerNorms later; the output is stored as usual.
+//   order (group > 1): 0 sums each pixel's band in ascending channel order
+//       in one wave, the LayerNorm kernels' order; 1 has every wave of the
+//       group sum its own channels, the group's partial sums then added in
+//       wave order (other bits: rounding differs).
 struct LnOut {
     const float *scale, *bias;
     float *y;
     float eps;
-    int32_t row0, keep, group, mode, nband, pad;
+    int32_t row0, keep, group, mode, nband, order;
 };
 
 struct GemmArgs {

@@ -534,37 +534,9 @@ __device__ void body(const GemmArgs &a, int ux, int nx, int by) {
             };
             const int band = lnw ? (w0 - a.lo.row0) / (G * TW) : 0;
             const int lq = lnw ? (w0 - a.lo.row0) / TW - band * G : 0;  // place in the group
-            sync();
-            if (lnw && lq == 0 && lane < PC) {
-                float s1 = 0.0f, s2 = 0.0f;
-                for (int q = 0; q < G; ++q) {
-#pragma unroll 8
-                    for (int c = 0; c < TW; ++c) {
-                        const float v = t[q * PER + c * LDT + lane];
-                        s1 += v;
-                        s2 += v * v;
-                    }
-                }
-                const float nf = (float)(G * TW);
-                const float m = s1 / nf;
-                const float var = s2 / nf - m * m;
-                const float r = 1.0f / sqrtf(fmaxf(var, 0.0f) + a.lo.eps);
-                if (a.lo.mode) {  // the statistics only, at the pixel's image position
-                    const int n = s0 + (KS == 1 ? lane : 16 * wave + lane);
-                    if (n < N) {
-                        float *sy = a.lo.y + (int64_t)band * 2 * N;
-                        const int64_t at = placed(n);
-                        sy[at] = m;
-                        sy[N + at] = r;
-                    }
-                } else {
-                    t[TW * LDT + lane] = m;
-                    t[TW * LDT + PC + lane] = r;
-                }
-            }
-            if (!a.lo.mode) sync();
-            if (lnw && !a.lo.mode) {
-                const float *ts = t - lq * PER + TW * LDT;  // the group's statistics
+            // mode 0: this wave's values of the band, normalised with the
+            // statistics at ts (mean row, then 1 / std row) and stored
+            auto normalise = [&](const float *ts) {
                 float lw[TMW], lb[TMW];
 #pragma unroll
                 for (int mt = 0; mt < TMW; ++mt) {
@@ -587,6 +559,81 @@ __device__ void body(const GemmArgs &a, int ux, int nx, int by) {
                     y.w = (y.w - m4.w) * r4.w * w + c;
                     st4(ly + off, y);
                 }
+            };
+            const float nf = (float)(G * TW);
+            auto stats = [&](float s1, float s2, int n_at) {
+                const float m = s1 / nf;
+                const float var = s2 / nf - m * m;
+                const float r = 1.0f / sqrtf(fmaxf(var, 0.0f) + a.lo.eps);
+                if (a.lo.mode) {  // the statistics only, at the pixel's image position
+                    const int n = s0 + n_at;
+                    if (n < N) {
+                        float *sy = a.lo.y + (int64_t)band * 2 * N;
+                        const int64_t at = placed(n);
+                        sy[at] = m;
+                        sy[N + at] = r;
+                    }
+                } else {
+                    t[TW * LDT + lane] = m;
+                    t[TW * LDT + PC + lane] = r;
+                }
+            };
+            if (KS == 1 && TW >= 32 && G > 1 && a.lo.order) {
+                // Each wave of the group sums its own channels of a pixel
+                // (its own LDS rows: a wave barrier), the partial sums meet
+                // in LDS (one block barrier), and every wave adds the
+                // group's partials in wave order and keeps the statistics
+                // it needs (its own rows again). A wave's partial sums of
+                // pixel p sit in its tile's row padding: s1 in rows 0..15,
+                // s2 in rows 16..31, column PC + p % 4 of row p / 4 (the
+                // padding holds 4 TW >= 2 PC floats and is read nowhere else).
+                auto pad = [&](int which, int p) { return (which * 16 + (p >> 2)) * LDT + PC + (p & 3); };
+                __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+                __builtin_amdgcn_wave_barrier();
+                __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+                if (lnw) {
+                    float p1 = 0.0f, p2 = 0.0f;
+#pragma unroll 8
+                    for (int c = 0; c < TW; ++c) {
+                        const float v = t[c * LDT + lane];
+                        p1 += v;
+                        p2 += v * v;
+                    }
+                    t[pad(0, lane)] = p1;
+                    t[pad(1, lane)] = p2;
+                }
+                __syncthreads();
+                if (lnw) {
+                    const float *g0 = t - lq * PER;
+                    float s1 = g0[pad(0, lane)], s2 = g0[pad(1, lane)];
+                    for (int q = 1; q < G; ++q) {
+                        s1 = s1 + g0[q * PER + pad(0, lane)];
+                        s2 = s2 + g0[q * PER + pad(1, lane)];
+                    }
+                    if (!a.lo.mode || lq == 0) stats(s1, s2, KS == 1 ? lane : 16 * wave + lane);
+                }
+                if (!a.lo.mode) {
+                    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+                    __builtin_amdgcn_wave_barrier();
+                    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+                }
+                if (lnw && !a.lo.mode) normalise(t + TW * LDT);
+            } else {
+                sync();
+                if (lnw && lq == 0 && lane < PC) {
+                    float s1 = 0.0f, s2 = 0.0f;
+                    for (int q = 0; q < G; ++q) {
+#pragma unroll 8
+                        for (int c = 0; c < TW; ++c) {
+                            const float v = t[q * PER + c * LDT + lane];
+                            s1 += v;
+                            s2 += v * v;
+                        }
+                    }
+                    stats(s1, s2, KS == 1 ? lane : 16 * wave + lane);
+                }
+                if (!a.lo.mode) sync();
+                if (lnw && !a.lo.mode) normalise(t - lq * PER + TW * LDT);  // the group's statistics
             }
         }
     }
