@@ -78,6 +78,21 @@ __device__ void body(const ConvArgs &a) {
 
     float4 wr[NW];
     float hr[XV ? 1 : NH];
+    // Generic halo: this thread's elements e = tid + 256 i as (channel within
+    // the chunk, offset c * plane + iy * wd + ix from the chunk's first plane;
+    // -1 outside the image or the halo), fixed for the block, so a chunk's
+    // fetch is unconditional loads from clamped addresses and selects (no
+    // per-element branches, whose exec masks would crowd the scalar registers).
+    int hc[XV ? 1 : NH], ho[XV ? 1 : NH];
+    if (!XV) {
+#pragma unroll
+        for (int i = 0; i < NH; ++i) {
+            const int e = tid + i * 256, c = e / (HH * HW), r = e % (HH * HW);
+            const int iy = iy0 + r / HW, ix = ix0 + r % HW;
+            hc[i] = c;
+            ho[i] = (e < HALO && iy >= 0 && iy < a.h && ix >= 0 && ix < a.wd) ? c * (int)plane + iy * a.wd + ix : -1;
+        }
+    }
     // XV: this thread's 128-bit loads (channel c, halo row r, quarter k) and
     // edge column, as element offsets from the chunk's first channel plane
     // (-1: outside the image, stored as zeros) and LDS offsets.
@@ -115,17 +130,13 @@ __device__ void body(const ConvArgs &a) {
             }
             er = (eoff >= 0 && tid / (HH * 2) < cmax) ? xc[eoff] : 0.0f;
         } else {
+            const float *xc = a.x + (int64_t)c0 * plane;  // chunk < nchunk: c0 < ci
+            const int cmax = a.ci - c0;
 #pragma unroll
             for (int i = 0; i < NH; ++i) {
-                const int e = tid + i * 256;
-                float v = 0.0f;
-                if (e < HALO) {
-                    const int c = e / (HH * HW), r = e % (HH * HW);
-                    const int iy = iy0 + r / HW, ix = ix0 + r % HW;
-                    if (c0 + c < a.ci && iy >= 0 && iy < a.h && ix >= 0 && ix < a.wd)
-                        v = a.x[(c0 + c) * plane + (int64_t)iy * a.wd + ix];
-                }
-                hr[i] = v;
+                const bool ok = ho[i] >= 0 && hc[i] < cmax;
+                const float v = xc[ok ? ho[i] : 0];
+                hr[i] = ok ? v : 0.0f;
             }
         }
     };
@@ -304,21 +315,32 @@ MXK_CONV4(128, 4, 4, 1)
 // 3x3 pad 1 with at most four output channels (the stage outputs to RGB): on
 // the vector ALUs, where an MFMA tile would be 3/16 useful. A block owns an
 // 8 x 8 output tile; its four waves split the input channels (wave w takes
-// c = w, w + 4, ...), each staging its channel's 10 x 10 halo in its own LDS
-// rows (no block barrier) with the next channel's halo already in registers,
-// and each lane accumulates its pixel's outputs (weights are wave-uniform,
-// read through the scalar cache); the four partial sums are added in LDS in
-// a fixed order (wave 0 + 1 + 2 + 3), then bias and the epilogue.
+// c = w, w + 4, ...), each staging a group of its channels' 10 x 10 halos in
+// its own LDS rows (no block barrier) with the next group's halos already in
+// flight, and each lane accumulates its pixel's outputs (weights are
+// wave-uniform, read through the scalar cache) in ascending channel order;
+// the four partial sums are added in LDS in a fixed order (wave 0 + 1 + 2 +
+// 3), then bias and the epilogue. The grid is one-dimensional (gridDim.y = 1).
 namespace conv {
 
 template <bool FUSED>
 __device__ void co4(const ConvArgs &a) {
-    __shared__ float halo[4][100];
+    // A wave takes its channels CG at a time (channels w, w + 4, ... in
+    // groups of CG consecutive ones of its own), the next group's halos in
+    // flight while the current group is multiplied.
+    constexpr int CG = 4;
+    __shared__ float halo[4][CG][100];
     __shared__ float part[4][4][64];
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int tiles_x = (a.wd + 7) / 8;
-    const int ty0 = (blockIdx.x / tiles_x) * 8, tx0 = (blockIdx.x % tiles_x) * 8;
+    // each XCD walks one contiguous run of tiles (row-major), so the tiles
+    // whose halos share cache lines (left-right neighbours share a 128-byte
+    // line four tiles wide, rows above and below share halo rows) are
+    // fetched into the same L2
+    int tile, band;
+    xcd_tile(tile, band);
+    const int ty0 = (tile / tiles_x) * 8, tx0 = (tile % tiles_x) * 8;
     const int py = lane / 8, px = lane % 8;
     const int64_t plane = (int64_t)a.h * a.wd;
     // the halo elements this lane stages: e = lane and lane + 64 (< 100)
@@ -328,32 +350,52 @@ __device__ void co4(const ConvArgs &a) {
         const int e = lane + 64 * k, iy = ty0 - 1 + e / 10, ix = tx0 - 1 + e % 10;
         hoff[k] = (e < 100 && iy >= 0 && iy < a.h && ix >= 0 && ix < a.wd) ? iy * a.wd + ix : -1;
     }
-    auto fetch = [&](int c, float *r) {
+    // group g of this wave: channels (4 g + wave) ... in steps of 4 (the
+    // wave's g-th run of CG of its own channels)
+    auto chan = [&](int g, int j) { return 4 * (CG * g + j) + wave; };
+    auto fetch = [&](int g, float *r) {
 #pragma unroll
-        for (int k = 0; k < 2; ++k) r[k] = (c < a.ci && hoff[k] >= 0) ? a.x[c * plane + hoff[k]] : 0.0f;
+        for (int j = 0; j < CG; ++j) {
+            const int c = chan(g, j);
+#pragma unroll
+            for (int k = 0; k < 2; ++k) {
+                const bool ok = c < a.ci && hoff[k] >= 0;
+                const float v = a.x[(ok ? c : 0) * plane + (ok ? hoff[k] : 0)];
+                r[2 * j + k] = ok ? v : 0.0f;
+            }
+        }
     };
     float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-    float cur[2], nxt[2];
-    fetch(wave, cur);
-    for (int c = wave; c < a.ci; c += 4) {
-        fetch(c + 4, nxt);
-        halo[wave][lane] = cur[0];
-        if (lane < 36) halo[wave][lane + 64] = cur[1];
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-        const float *w = a.w + (int64_t)c * 36;  // [c][tap][4]: wave-uniform
+    float cur[2 * CG], nxt[2 * CG];
+    const int ng = (a.ci + 4 * CG - 1) / (4 * CG);  // groups (every wave takes the same count)
+    fetch(0, cur);
+    for (int g = 0; g < ng; ++g) {
+        if (g + 1 < ng) fetch(g + 1, nxt);
 #pragma unroll
-        for (int tap = 0; tap < 9; ++tap) {
-            const float xv = halo[wave][(py + tap / 3) * 10 + px + tap % 3];
-#pragma unroll
-            for (int o = 0; o < 4; ++o) acc[o] = __builtin_fmaf(w[tap * 4 + o], xv, acc[o]);
+        for (int j = 0; j < CG; ++j) {
+            halo[wave][j][lane] = cur[2 * j];
+            if (lane < 36) halo[wave][j][lane + 64] = cur[2 * j + 1];
         }
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-        cur[0] = nxt[0];
-        cur[1] = nxt[1];
+#pragma unroll
+        for (int j = 0; j < CG; ++j) {
+            const int c = chan(g, j);
+            if (c >= a.ci) break;  // wave-uniform
+            const float *w = a.w + (int64_t)c * 36;  // [c][tap][4]: wave-uniform
+#pragma unroll
+            for (int tap = 0; tap < 9; ++tap) {
+                const float xv = halo[wave][j][(py + tap / 3) * 10 + px + tap % 3];
+#pragma unroll
+                for (int o = 0; o < 4; ++o) acc[o] = __builtin_fmaf(w[tap * 4 + o], xv, acc[o]);
+            }
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+        for (int k = 0; k < 2 * CG; ++k) cur[k] = nxt[k];
     }
 #pragma unroll
     for (int o = 0; o < 4; ++o) part[o][wave][lane] = acc[o];
