@@ -86,7 +86,7 @@ struct Launch {
     unsigned g[3] = {1, 1, 1};
     unsigned b[3] = {MXK_BLOCK, 1, 1};
     unsigned shm = 0;  // dynamic LDS bytes
-    alignas(16) unsigned char a0[768];
+    alignas(16) unsigned char a0[1024];
     alignas(16) unsigned char a1[32];
     int nparams = 1;
     int kind = 0;  // 1: a0 holds GemmArgs (plain epilogue), 2: ConvArgs, 3: DualGemmArgs
@@ -661,9 +661,19 @@ private:
     // when its shape and alignment allow them; `layout` 0 = channel-major
     // output, 1 = row-major. `alt` keeps the tiled-GEMM launch of each op that
     // got one, for fused steps whose extra operands are not 16-byte aligned.
-    bool try_pw(int layout, const GemmArgs &a, Launch &l, bool whole = false) {
+    // fold (channel-major, batch > 1): tile the batches' columns as one axis
+    // (GemmArgs fold), so a batch of N columns that is not a multiple of 64
+    // leaves no ragged tile per batch.
+    bool try_pw(int layout, const GemmArgs &a0, Launch &l, bool whole = false, bool fold = false) {
         if (no_pw) return false;
-        const int64_t wout = layout == 0 ? a.M : a.N, slen = layout == 0 ? a.N : a.M;
+        GemmArgs a = a0;
+        fold = fold && layout == 0 && a.batch > 1 && a.N % 4 == 0 && a.N % 64 != 0 &&
+               (int64_t)a.batch * a.N < 0x7fffffffLL && a.sC == (int64_t)a.M * a.N;
+        if (fold) {
+            a.fold = a.N;
+            div_magic((uint32_t)a.N, a.fmul, a.fsh);
+        }
+        const int64_t wout = layout == 0 ? a.M : a.N, slen = layout == 0 ? (fold ? (int64_t)a.batch * a.N : a.N) : a.M;
         if (a.K % 16 || a.N % 4 || a.K == 0 || wout <= 0 || slen <= 0) return false;
         if (!aligned(a.A, 16) || !aligned(a.B, 16) || !aligned(a.C, 16)) return false;
         if (layout == 1 && !aligned(a.bias, 16)) return false;
@@ -684,12 +694,13 @@ private:
         // whole: the reduction stays in one wave (a step whose epilogue
         // normalises bands across several waves of a block, which needs them
         // to hold whole tiles)
-        const bool k4 = !whole && a.K % 64 == 0 && (a.K >= 128 || tiles * a.batch < 2LL * 4 * cus);
-        l = mk(std::string(names[layout][ti]) + (k4 ? "_k4" : ""));
+        const int64_t nbat = fold ? 1 : a.batch;
+        const bool k4 = !whole && a.K % 64 == 0 && (a.K >= 128 || tiles * nbat < 2LL * 4 * cus);
+        l = mk(std::string(names[layout][ti]).insert(8, fold ? "b" : "") + (k4 ? "_k4" : ""));
         const int64_t grid = k4 ? tiles : (tiles + 3) / 4;
         if (grid > 0x7fffffffLL) return false;
         l.g[0] = (unsigned)grid;
-        l.g[1] = (unsigned)a.batch;
+        l.g[1] = (unsigned)nbat;
         l.kind = 1;
         set_args(l, a);
         return true;
@@ -1365,7 +1376,7 @@ void Gpu::build_launches(const mx_plan_desc *p, const std::vector<int64_t> &woff
                     set_args(l, a);
                     l.kind = 1;
                     Launch q;
-                    if (try_pw(0, a, q)) {
+                    if (try_pw(0, a, q, false, true)) {
                         alt[i].push_back(l);
                         L.push_back(q);
                     } else {

@@ -220,6 +220,13 @@ struct GemmArgs {
     BlockMap ymap, xmap;
     const float *B2;      // _mul: X is B * B2 elementwise (a folded Mul), same layout
     LnOut lo;
+    // Channel-major with batch > 1: fold > 0 tiles the batch's columns as
+    // one axis of batch * N columns (N = fold, a multiple of 4, so four
+    // consecutive columns lie in one batch); column n is column n % fold of
+    // batch n / fold (n / fold = umulhi(2 n, fmul) >> fsh, as BlockMap's).
+    // The grid is then one-dimensional.
+    int32_t fold, fsh;
+    uint32_t fmul, pad2;
 };
 
 // Two independent streaming-GEMM launches of one kernel in one grid: blocks

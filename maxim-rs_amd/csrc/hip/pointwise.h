@@ -80,7 +80,7 @@ enum { EP_U = 1, EP_R1 = 2, EP_R2 = 4, EP_GELU = 8, EP_LRELU = 16, EP_YMAP = 32,
 // (ux, nx): this block's index and the block count along x, by: the batch;
 // a kernel pairing two launches in one grid passes each part its own.
 template <int LAYOUT, int TMW, int KS, bool FUSED, int LN, bool XM = false, bool XMUL = false, bool CT = false,
-          bool LNO = false, int EP = -1>
+          bool LNO = false, int EP = -1, bool FOLD = false>
 __device__ void body(const GemmArgs &a, int ux, int nx, int by) {
     const bool has_u = EP < 0 ? a.e.u != nullptr : (EP & EP_U) != 0;
     const bool has_r1 = EP < 0 ? a.e.r1 != nullptr : (EP & EP_R1) != 0;
@@ -97,10 +97,14 @@ __device__ void body(const GemmArgs &a, int ux, int nx, int by) {
     const int i = lane & 15, g = lane >> 4;
     const int M = a.M, N = a.N, K = a.K;
     const int wout = LAYOUT == CH ? M : N;
-    const int slen = LAYOUT == CH ? N : M;
+    // CH with the batch folded into the columns: batch * N columns, batch
+    // n / N holding column n (whole 4-column groups; the grid is 1-D)
+    static_assert(!FOLD || (LAYOUT == CH && !LN && !CT && !LNO && !XMUL), "a folded batch: GateMm mode 0");
+    constexpr bool fold = FOLD;
+    const int slen = LAYOUT == CH ? (fold ? a.batch * N : N) : M;
     const int nib = (wout + TW - 1) / TW;
     const int ntiles = nib * ((slen + 63) / 64);  // < 2^31, checked by the host
-    const int b = by;
+    const int b = fold ? 0 : by;
     const float *W = a.A + (int64_t)b * a.sA;
     const float *X = a.B + (int64_t)b * a.sB;
     float *Y = a.C + (int64_t)b * a.sC;
@@ -143,10 +147,17 @@ __device__ void body(const GemmArgs &a, int ux, int nx, int by) {
         const uint32_t fy = mdiv(c, xm.mfw, xm.sfw), fx = c - fy * (uint32_t)xm.fw;
         return (int64_t)fy * xm.wd + fx;
     };
-    // CH: this lane's four columns, s0 + 16 (i % 4) + 4 (i / 4) .. + 3
+    // CH: this lane's four columns, s0 + 16 (i % 4) + 4 (i / 4) .. + 3 (with
+    // a folded batch: column xcol of batch xb)
     int xcol = 0;
+    int64_t xbo = 0;  // the folded batch's X offset
     if (LAYOUT == CH) {
-        xcol = min(s0 + 16 * (i & 3) + 4 * (i >> 2), N - 4);
+        xcol = min(s0 + 16 * (i & 3) + 4 * (i >> 2), slen - 4);
+        if (fold) {
+            const uint32_t xb = mdiv((uint32_t)xcol, a.fmul, a.fsh);
+            xcol -= (int)xb * N;
+            xbo = (int64_t)xb * a.sB;
+        }
         if (LN && xm.on) xcol = (int)unblock(xm, (uint32_t)xcol);
     }
     const float *xp[4];
@@ -154,9 +165,9 @@ __device__ void body(const GemmArgs &a, int ux, int nx, int by) {
     for (int q = 0; q < 4; ++q) {
         if (LAYOUT == CH) {  // row k = 16 S + 4 g + q
             if (XM)
-                xp[q] = X + cell(16 * S0 + 4 * g + q) + pixel(xcol);
+                xp[q] = X + xbo + cell(16 * S0 + 4 * g + q) + pixel(xcol);
             else
-                xp[q] = X + (int64_t)(4 * g + q) * N + xcol + S0 * xstep;
+                xp[q] = X + xbo + (int64_t)(4 * g + q) * N + xcol + S0 * xstep;
         } else {  // row s0 + 16 q + i, k = 16 S + 4 g .. + 3
             const int row = min(s0 + 16 * q + i, M - 1);
             if (XM)
@@ -327,6 +338,11 @@ __device__ void body(const GemmArgs &a, int ux, int nx, int by) {
         const int mt = KS == 1 ? k / 4 : k, x = KS == 1 ? k % 4 : wave;
         if (LAYOUT == CH) {
             const int m = w0 + mt * 16 + i, n = s0 + 16 * x + 4 * g;
+            if (fold) {  // batch nb, column n - nb N of it
+                const uint32_t nb = mdiv((uint32_t)min(n, slen - 4), a.fmul, a.fsh);
+                off = (int64_t)nb * a.sC + (int64_t)(w0 + i + mt * 16) * N + (n - (int)nb * N);
+                return m < M && n < slen;
+            }
             off = obase + (int64_t)(mt * 16) * N + 16 * x;
             return m < M && n < N;
         }
@@ -677,6 +693,20 @@ MXK_PW1(ch, CH, 2, 4, 2, false, _k4_ln2)
 MXK_PW(ch, CH, 1)
 MXK_PW(ch, CH, 2)
 MXK_PW(ch, CH, 4)
+// mx_pw_chb<TMW>[_k4][_xm][_f]: channel-major over a folded batch (GemmArgs
+// fold; GateMm mode 0, whose channels are the batch)
+#define MXK_PWB1(TMW, KS, XM, SUF)                                                                  \
+    extern "C" __global__ __launch_bounds__(256) void mx_pw_chb##TMW##SUF(GemmArgs a) {             \
+        pw::body<pw::CH, TMW, KS, false, 0, XM, false, false, false, -1, true>(a, blockIdx.x, gridDim.x, 0); \
+    }                                                                                               \
+    extern "C" __global__ __launch_bounds__(256) void mx_pw_chb##TMW##SUF##_f(GemmArgs a) {         \
+        pw::body<pw::CH, TMW, KS, true, 0, XM, false, false, false, -1, true>(a, blockIdx.x, gridDim.x, 0); \
+    }
+#define MXK_PWB(TMW) \
+    MXK_PWB1(TMW, 1, false, ) MXK_PWB1(TMW, 4, false, _k4) MXK_PWB1(TMW, 1, true, _xm) MXK_PWB1(TMW, 4, true, _k4_xm)
+MXK_PWB(1)
+MXK_PWB(2)
+MXK_PWB(4)
 MXK_PW(rw, RW, 1)
 MXK_PW(rw, RW, 2)
 MXK_PW(rw, RW, 4)
@@ -748,6 +778,9 @@ MXK_PW_E(mx_pw_ch2_mul_f, CH, 2, 1, 0, false, true, false, 70)
 MXK_PW_E(mx_pw_ch2_k4_mul_f, CH, 2, 4, 0, false, true, false, 66)
 MXK_PW_E(mx_pw_ch2_k4_mul_f, CH, 2, 4, 0, false, true, false, 70)
 MXK_PW_E(mx_pw_rw2_k4_f, RW, 2, 4, 0, false, false, false, 65)
+extern "C" __global__ __launch_bounds__(256) void mx_pw_chb2_k4_f_e65(GemmArgs a) {
+    pw::body<pw::CH, 2, 4, true, 0, false, false, false, false, 65, true>(a, blockIdx.x, gridDim.x, 0);
+}
 MXK_PW_E(mx_pw_rw4_k4_f, RW, 4, 4, 0, false, false, false, 65)
 MXK_PW_X2(mx_pw_ch2_ln_f_lo, CH, 2, 1, 1, false, false, true, 72)
 MXK_PW_X2(mx_pw_ch1_f, CH, 1, 1, 0, false, false, false, 226)

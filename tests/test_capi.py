@@ -60,6 +60,10 @@ def test_the_code_object_is_embedded_and_complete():
     launched |= {"mx_pw_ch%d%s_ln%s" % (t, k, f) for t in (1, 2, 4) for k in ("", "_k4") for f in ("", "_f")}
     launched |= {"mx_pw_%s%d%s_xm%s" % (l, t, k, f) for l in ("ch", "rw") for t in (1, 2, 4)
                  for k in ("", "_k4") for f in ("", "_f")}
+    # the channel-major forms over a folded batch (GateMm mode 0)
+    launched |= {"mx_pw_chb%d%s%s%s" % (t, k, x, f) for t in (1, 2, 4) for k in ("", "_k4") for x in ("", "_xm")
+                 for f in ("", "_f")}
+    launched |= {"mx_pw_chb2_k4_f_e65"}
     launched |= {"mx_pw_ch%d%s_mul%s" % (t, k, f) for t in (1, 2, 4) for k in ("", "_k4") for f in ("", "_f")}
     launched |= {"mx_pw_ch%d%s_t" % (t, k) for t in (1, 2, 4) for k in ("", "_k4")}
     launched |= {"mx_pw_ch%d%s%s_f_lo" % (t, k, l) for t in (2, 4) for k in ("", "_k4") for l in ("", "_ln")}
