@@ -5,6 +5,12 @@
                    every op's destination is compared (bar: max|d| <= 1e-3 *
                    max|cpu|, src/main.rs:709-712); the first failures are
                    reported with the op, its buffer label and the element.
+  verify_program_walk
+                   the same lockstep check over the FUSED program the timed
+                   path runs (no counterpart in the reference, which launches
+                   one kernel per op): step by step, each step given the CPU
+                   path's exact inputs, every buffer the step leaves for a
+                   later op compared.
   timeline_report  the --profile census (src/main.rs:526-656): device time
                    per op family, per op shape (the 12 most expensive and
                    every shape with 16 or more ops) and the five slowest ops,
@@ -104,6 +110,86 @@ def verify_walk(plan, image, cpu_step, judge=None, resync=False, tol=1e-3, max_r
             out("verify: %d ops, %d disagree beyond the bar (worst %.3e relative)" % (len(plan.ops), bad, worst))
         return {"ops": len(plan.ops), "bad": bad, "worst": worst, "worst_by_key": by_key,
                 "first": failures[0] if failures else None, "failures": failures}
+    finally:
+        gpu.close()
+
+
+def verify_program_walk(plan, image, cpu_step, tol=1e-4, max_report=20, out=None):
+    """The fused program (mxh_steps: fused launches, paired branches,
+    folded LayerNorms and permutations, commuted resizes; the default
+    arithmetic order, not MAXIM_PLAN_ORDER=1) stepped against the CPU path.
+
+    Before each step the device receives the CPU path's exact values of
+    every buffer the step's ops read from earlier ops (for a permutation the
+    executor elides, whose readers take its source through a map, that
+    source); the step runs as it runs in a pass (mxh_run_ops over its op
+    range: a folded LayerNorm whose statistics an earlier step wrote gets
+    its statistics pass first), the CPU path runs the step's ops, and every
+    buffer the step writes that a later op reads, or the plan's output, is
+    judged: max|d| <= tol * max|cpu|. Buffers inside a step are never
+    materialised and an elided permutation's output is never written, so
+    neither is compared. Returns a dict: steps, compared (buffers), bad,
+    worst, worst_by_kernel (by the kernel naming each step), kernels (every
+    kernel the program launches), failures (the first `max_report`)."""
+    from . import hip as H
+    img = np.ascontiguousarray(image, np.float32)
+    arena = np.zeros(plan.arena_len, np.float32)
+    o = int(plan.offs[plan.input])
+    arena[o:o + img.size] = img.ravel()
+    last_read = {}
+    for i, op in enumerate(plan.ops):
+        for s in op_sources(plan, op):
+            last_read[s] = i
+    gpu = H.Gpu(plan)
+    try:
+        gpu.begin(img)
+        steps = gpu.steps()
+        elided = {plan.ops[a].dst: plan.ops[a].src for a, b, k in steps
+                  if not k and b == a + 1 and plan.ops[a].kind == P.BLOCK_PERM}
+        worst, by_kernel, failures, bad, compared = 0.0, {}, [], 0, 0
+        for n, (a, b, kernel) in enumerate(steps):
+            made = set()
+            for i in range(a, b):
+                for s in op_sources(plan, plan.ops[i]):
+                    if s in made:
+                        continue
+                    while s in elided:
+                        s = elided[s]
+                    gpu.write_buf(s, _buf(plan, arena, s))
+                made.add(plan.ops[i].dst)
+            for i in range(a, b):
+                cpu_step(plan, arena, i)
+            gpu.run_ops(a, b)
+            for d in sorted(made):
+                if d in elided or not (last_read.get(d, -1) >= b or d == plan.output):
+                    continue
+                want = _buf(plan, arena, d)
+                got = gpu.read_buf(d)
+                diff = np.abs(got.astype(np.float64) - want)
+                scale = max(float(np.abs(want).max()) if want.size else 0.0, 1e-6)
+                at = int(diff.argmax()) if diff.size else 0
+                rel = float(diff[at]) / scale if diff.size else 0.0
+                if not np.isfinite(got).all():
+                    rel = float("inf")
+                compared += 1
+                worst = max(worst, rel)
+                key = kernel or "(no launch)"
+                by_kernel[key] = max(by_kernel.get(key, 0.0), rel)
+                if not rel <= tol:
+                    bad += 1
+                    rec = {"step": n, "ops": (a, b), "kernel": kernel, "buf": int(d), "relative": rel,
+                           "element": at, "describe": plan.ops[b - 1].describe()}
+                    if len(failures) < max_report:
+                        failures.append(rec)
+                        if out:
+                            out("step %d (ops %d-%d, %s): #%d differs by %.4e relative (element %d)"
+                                % (n, a, b - 1, kernel, d, rel, at))
+        if out:
+            out("program walk: %d steps, %d buffers compared, %d beyond the bar (worst %.3e relative)"
+                % (len(steps), compared, bad, worst))
+        return {"steps": len(steps), "compared": compared, "bad": bad, "worst": worst,
+                "worst_by_kernel": by_kernel, "kernels": sorted({k for _, k in gpu.launches()}),
+                "failures": failures}
     finally:
         gpu.close()
 

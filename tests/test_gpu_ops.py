@@ -14,6 +14,9 @@ BIT-EXACT:
   rounding  chan_mean (tree vs serial order) and every matrix-core GEMM
             (conv1x1, conv3x3, conv4x4s2, convt2x2, gate_mm):
             max|d| <= 1e-4 * max|cpu| (ten times tighter than the reference's bar)
+
+The same check over the fused program the timed path runs (its steps, each
+on the CPU path's exact inputs, every buffer a step hands on) at the GEMM bar.
 """
 
 import numpy as np
@@ -98,3 +101,63 @@ def test_verify_walk_names_the_first_wrong_op(gpu_ok):
 
     r = D.verify_walk(plan, smooth_image(64, 64, seed=6), planted)
     assert r["bad"] >= 1 and r["first"]["op"] == bad_op and r["first"]["element"] == 17, r["first"]
+
+
+def program_walk(plan, img, out=print):
+    from maxim_amd import devtools as D
+    from oracle import oracle as O
+    return D.verify_program_walk(plan, img, O.step, tol=1e-4, out=out)
+
+
+@pytest.mark.parametrize("variant,h,w", [("S-2", 64, 64), ("S-3", 128, 192)])
+def test_fused_program_matches_the_cpu_path_step_by_step(gpu_ok, variant, h, w):
+    """The program the timed path runs (fused epilogues, folded LayerNorms
+    and permutations, split reductions, the default arithmetic order), step
+    by step on the CPU path's exact inputs: every buffer a step hands to a
+    later op within the GEMM bar, 1e-4 * max|cpu|."""
+    from maxim_amd import plan as P
+    plan = P.Plan(weights(variant), h, w)
+    r = program_walk(plan, smooth_image(h, w, seed=4))
+    print("worst by kernel", sorted(r["worst_by_kernel"].items(), key=lambda kv: -kv[1])[:8])
+    assert r["compared"] > 0.4 * r["steps"] and r["bad"] == 0, r["failures"][:5]
+
+
+def test_fused_program_walk_at_c4(gpu_ok):
+    """The same step-by-step check at the headline size (MAXIM-3S, 448x640
+    padded), where the executor also pairs the gMLP branches' launches, tiles
+    the GateMm batches as one axis and commutes UpSampleRatio's resize and
+    conv: the exact launches the bench times, each step judged on its own."""
+    from maxim_amd import plan as P
+    plan = P.Plan(weights("S-3"), 448, 640)
+    print("program walk S-3 448x640, %d ops" % len(plan.ops), flush=True)
+    r = program_walk(plan, smooth_image(448, 640, seed=6))
+    kinds = r["kernels"]
+    print("worst by kernel", sorted(r["worst_by_kernel"].items(), key=lambda kv: -kv[1])[:8])
+    assert r["bad"] == 0, r["failures"][:5]
+    assert any(k.endswith("_x2") for k in kinds) and any(k.startswith("mx_pw_chb") for k in kinds), kinds
+
+
+def test_program_walk_names_the_step_of_a_wrong_op(gpu_ok):
+    """A mistake planted in the CPU path inside a fused step (the first op's
+    destination, which the step never materialises, shifted by 1e-2 of its
+    scale) is reported at that step: the step's outputs carry it."""
+    from maxim_amd import devtools as D
+    from maxim_amd import hip as H
+    from maxim_amd import plan as P
+    from oracle import oracle as O
+    plan = P.Plan(weights("S-2"), 64, 64)
+    gpu = H.Gpu(plan)
+    steps = gpu.steps()
+    gpu.close()
+    multi = [(a, b) for a, b, k in steps if b - a >= 3 and k.startswith("mx_pw_")]
+    a, b = multi[len(multi) // 2]
+
+    def planted(pl, arena, i):
+        O.step(pl, arena, i)
+        if i == a:
+            o = int(pl.offs[pl.ops[i].dst])
+            seg = arena[o:o + pl.buf_len(pl.ops[i].dst)]
+            seg[17] += 1e-2 * max(float(np.abs(seg).max()), 1e-3)
+
+    r = D.verify_program_walk(plan, smooth_image(64, 64, seed=6), planted)
+    assert r["bad"] >= 1 and r["failures"][0]["ops"] == (a, b), (a, b, r["failures"][:2])
