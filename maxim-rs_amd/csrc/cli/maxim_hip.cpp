@@ -1,13 +1,18 @@
 // maxim_hip: the enhancement run on one MI355X, the reference CLI's `run`
-// (src/main.rs:173-458) with the HIP backend:
+// (src/main.rs:173-458) with the HIP backend, and its argument handling
+// (src/main.rs:59-158) as a release build has it:
 //
 //   maxim_hip -m MODEL.safetensors [-i IN.png] [-o OUT.png] [-q]
 //
 // reads the PNG (from stdin when -i is `-` or absent, src/main.rs:205-214),
 // runs mxh_enhance (checkpoint -> padded plan -> device pass -> crop) and
 // writes the PNG (to stdout when -o is `-` or absent, src/main.rs:439-448).
-// As in the reference, a pass that fails is reported, not retried elsewhere;
-// there is no CPU backend in this binary.
+// As in the reference, a pass that fails is reported, not retried elsewhere.
+// There is no CPU backend in this binary: `--device gpu|hip` and `--gpu`
+// select the one it has, `--device cpu` and `--cpu` are refused by name.
+// The development flags (--dump, --profile, --factor) live in the Python
+// package's entry point (python -m maxim_amd); like the reference's release
+// build, this binary refuses them by name rather than ignoring them.
 
 #include <cerrno>
 #include <chrono>
@@ -18,13 +23,19 @@
 
 #include "maxim_hip.h"
 
+static const char *kVersion = "0.3.0";
+
 static int usage() {
     std::fprintf(stderr,
-                 "usage: maxim_hip -m MODEL.safetensors [-i IN.png] [-o OUT.png] [-q]\n"
+                 "usage: maxim_hip -m MODEL.safetensors [-i IN.png] [-o OUT.png] [options]\n"
                  "    -m, --model <path>    converted .safetensors checkpoint\n"
                  "    -i, --input <path>    input PNG, or - for stdin (default: stdin)\n"
                  "    -o, --output <path>   output PNG, or - for stdout (default: stdout)\n"
-                 "    -q, --quiet           no progress output\n");
+                 "        --device <dev>    gpu (or hip): the MI355X; this binary has no CPU backend\n"
+                 "        --gpu             same as --device gpu\n"
+                 "    -q, --quiet           no progress output\n"
+                 "    -h, --help            this text\n"
+                 "    -V, --version         print the version\n");
     return 2;
 }
 
@@ -43,16 +54,43 @@ int main(int argc, char **argv) {
             v = argv[++i];
             return true;
         };
-        if ((a == "-m" || a == "--model") && next(model)) continue;
-        if ((a == "-i" || a == "--input") && next(in)) continue;
-        if ((a == "-o" || a == "--output") && next(out)) continue;
-        if (a == "-q" || a == "--quiet") {
+        std::string dev;
+        if (a == "-m" || a == "--model") {
+            if (!next(model)) return usage();
+        } else if (a == "-i" || a == "--input") {
+            if (!next(in)) return usage();
+        } else if (a == "-o" || a == "--output") {
+            if (!next(out)) return usage();
+        } else if (a == "-q" || a == "--quiet") {
             quiet = true;
-            continue;
+        } else if (a == "--device" || a == "--gpu" || a == "--cpu") {
+            if (a == "--device" && !next(dev)) return usage();
+            if (a == "--cpu" || (a == "--device" && dev != "gpu" && dev != "hip")) {
+                std::fprintf(stderr, "maxim: `%s%s%s`: this binary runs on the MI355X only (no CPU backend)\n",
+                             a.c_str(), dev.empty() ? "" : " ", dev.c_str());
+                return 2;
+            }
+        } else if (a == "--dump" || a == "--profile" || a == "--timeline" || a == "--verify-gpu" ||
+                   a == "--factor") {
+            std::fprintf(stderr,
+                         "maxim: `%s` is a development flag and this is the release command\n"
+                         "maxim: python -m maxim_amd takes --dump, --profile and --factor\n",
+                         a.c_str());
+            return 2;
+        } else if (a == "-h" || a == "--help") {
+            return usage();
+        } else if (a == "-V" || a == "--version") {
+            std::printf("maxim_hip %s\n", kVersion);
+            return 0;
+        } else {
+            std::fprintf(stderr, "maxim: unknown argument `%s`\n", a.c_str());
+            return usage();
         }
+    }
+    if (model.empty()) {
+        std::fprintf(stderr, "maxim: --model is required\n");
         return usage();
     }
-    if (model.empty()) return usage();
     if (mxh_driver_ready() != 0) {
         std::fprintf(stderr, "maxim: hip: %s\n", mx_last_error());
         return 1;

@@ -97,3 +97,40 @@ def test_cli_stdin_stdout_interlaced(gpu_ok, tmp_path):
         out = P.read_png(data=r.stdout)
         assert out.shape == (3, 70, 90)
         assert np.abs(np.rint(out * 255) - want).max() <= 1.0
+
+
+def test_dev_entry_point_dump_profile(gpu_ok, tmp_path):
+    """`python -m maxim_amd` (the reference's dev build: src/main.rs with
+    --dump and --profile) gives the same PNG as `maxim_hip` on the same
+    checkpoint and image (byte for byte; with --dump the plan is built
+    `named`, whose kept buffers can change which ops fuse, so there within
+    one 8-bit level), writes every named activation as .npy and prints the
+    census; stdin/stdout work as they do for the command."""
+    import sys
+    from maxim_amd import plan as P
+    ckpt = str(tmp_path / "maxim_s2.safetensors")
+    weights("S-2").save(ckpt)
+    src = str(tmp_path / "in.png")
+    P.write_png(src, smooth_image(100, 140, seed=3))
+    exe = os.path.join(ROOT, "maxim-rs_amd", "lib", "maxim_hip")
+    ref_png = str(tmp_path / "ref.png")
+    r = subprocess.run([exe, "-m", ckpt, "-i", src, "-o", ref_png, "-q"], capture_output=True, text=True,
+                       timeout=300)
+    assert r.returncode == 0, r.stderr
+    env = dict(os.environ, PYTHONPATH=os.path.join(ROOT, "maxim-rs_amd"))
+    dump = str(tmp_path / "dump")
+    out_png = str(tmp_path / "out.png")
+    print("python -m maxim_amd --dump --profile", flush=True)
+    r = subprocess.run([sys.executable, "-m", "maxim_amd", "-m", ckpt, "-i", src, "-o", out_png,
+                        "--dump", dump, "--profile"], capture_output=True, text=True, timeout=600, env=env)
+    print(r.stderr[-3000:], flush=True)
+    assert r.returncode == 0, r.stderr
+    levels = np.abs(np.rint(P.read_png(out_png) * 255) - np.rint(P.read_png(ref_png) * 255))
+    assert levels.max() <= 1.0
+    files = sorted(os.listdir(dump))
+    assert len(files) >= 40 and all(f.endswith(".npy") for f in files), files[:5]
+    assert "fused program:" in r.stderr and "slowest ops:" in r.stderr
+    r = subprocess.run([sys.executable, "-m", "maxim_amd", "-m", ckpt, "-q"], input=open(src, "rb").read(),
+                       capture_output=True, timeout=600, env=env)
+    assert r.returncode == 0, r.stderr.decode()
+    assert r.stdout == open(ref_png, "rb").read()
