@@ -48,6 +48,18 @@ int mxh_run(mxh_gpu *g, const mx_plan_desc *plan, const float *input, uint64_t n
 int mxh_begin(mxh_gpu *g, const mx_plan_desc *plan, const float *input, uint64_t n_in);
 /* Gpu::step_op (src/exec_gpu.rs:348-352): execute exactly op `i`. */
 int mxh_step_op(mxh_gpu *g, const mx_plan_desc *plan, uint64_t i);
+/* No counterpart in the reference (one image per run): `n_images` images
+ * through the same plan for a serving loop, each image's pass exactly
+ * mxh_run's (so each output is mxh_run's to the bit), with the host's work
+ * off the device's path: image k's input is staged into pinned memory while
+ * pass k - 1 runs and image k - 1's output handed back while pass k runs, so
+ * the device only adds the two DMA copies per image. inputs[k] (n_in floats)
+ * and outputs[k] (n_out floats) are host arrays; every output is written
+ * when the call returns. The staging (two pinned buffers each way and their
+ * events) is allocated on the first call and kept with the executor. Not
+ * with the timeline on. */
+int mxh_run_batch(mxh_gpu *g, const mx_plan_desc *plan, const float *const *inputs, uint64_t n_in,
+                  float *const *outputs, uint64_t n_out, uint64_t n_images);
 /* No counterpart in the reference: for callers that cannot allocate device
  * memory (code under HIP graph capture, tight serving loops, harnesses that
  * forbid hipMalloc). mxh_run's pass with device-resident input and output

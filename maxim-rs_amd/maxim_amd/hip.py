@@ -64,6 +64,7 @@ def _lib():
             "mxh_device_info": (I, [V, C.POINTER(C.c_int), C.POINTER(C.c_int)]),
             "mxh_device_memory": (I, [C.POINTER(C.c_uint64), C.POINTER(C.c_uint64)]),
             "mxh_run_noalloc": (I, [V, D, V, U, V, U, V]),
+            "mxh_run_batch": (I, [V, D, C.POINTER(V), U, C.POINTER(V), U, U]),
             "mxh_time_graph": (I, [V, D, C.c_int, V]),
             "mxh_enhance": (I, [C.c_char_p, V, C.c_int64, C.c_int64, V]),
         }
@@ -127,6 +128,22 @@ class Gpu:
         out = np.empty((c, h, w), np.float32)
         _check(_lib().mxh_run(self._h, self._d, img.ctypes.data, img.size, out.ctypes.data, out.size))
         return out
+
+    def run_batch(self, images):
+        """mxh_run_batch: every image of the list through the pass, the
+        host's staging overlapped with the passes; the outputs, each
+        mxh_run's to the bit."""
+        imgs = [np.ascontiguousarray(im, dtype=np.float32) for im in images]
+        c, h, w = self.plan.bufs[self.plan.output]
+        outs = [np.empty((c, h, w), np.float32) for _ in imgs]
+        n_in = int(np.prod(self.plan.bufs[self.plan.input]))
+        for im in imgs:
+            if im.size != n_in:
+                raise P.MaximError("the input image and the plan's input buffer disagree")
+        ins = (C.c_void_p * max(len(imgs), 1))(*[im.ctypes.data for im in imgs])
+        ous = (C.c_void_p * max(len(outs), 1))(*[o.ctypes.data for o in outs])
+        _check(_lib().mxh_run_batch(self._h, self._d, ins, n_in, ous, c * h * w, len(imgs)))
+        return outs
 
     def run_noalloc(self, d_input, d_output, stream=None):
         """mxh_run_noalloc: the pass from device pointer d_input to d_output

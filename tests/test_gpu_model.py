@@ -245,3 +245,27 @@ def test_gmlp_branches_share_launches(gpu_ok):
     finally:
         del os.environ["MAXIM_NO_PAIR"]
     assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
+
+
+@pytest.mark.parametrize("variant,h,w,n,graph", [("S-2", 128, 192, 5, False), ("S-3", 448, 640, 3, True)])
+def test_run_batch_equals_run_per_image(gpu_ok, variant, h, w, n, graph):
+    """mxh_run_batch (pinned staging in two slots, the host's copies
+    overlapped with the passes): each image's output is mxh_run's to the
+    bit, for an odd count (the two staging slots alternate unevenly), with
+    eager launches and with graph replays; an empty list does nothing, and a
+    second batch on the same executor reuses the staging."""
+    from maxim_amd import plan as P
+    from maxim_amd import hip as H
+    plan = P.Plan(weights(variant), h, w)
+    imgs = [smooth_image(h, w, seed=30 + k) for k in range(n)]
+    gpu = H.Gpu(plan)
+    gpu.set_graph(graph)
+    want = [gpu.run(im).copy() for im in imgs]
+    print("%s %dx%d: %d images, graph %s" % (variant, w, h, n, graph), flush=True)
+    assert gpu.run_batch([]) == []
+    for rep in range(2):
+        got = gpu.run_batch(imgs if rep == 0 else imgs[::-1])
+        for k, g in enumerate(got):
+            ref = want[k] if rep == 0 else want[n - 1 - k]
+            assert np.array_equal(g.view(np.uint32), ref.view(np.uint32)), (rep, k)
+    gpu.close()
