@@ -786,3 +786,11 @@ MXK_PW_X2(mx_pw_ch2_ln_f_lo, CH, 2, 1, 1, false, false, true, 72)
 MXK_PW_X2(mx_pw_ch1_f, CH, 1, 1, 0, false, false, false, 226)
 MXK_PW_X2(mx_pw_ch2_f, CH, 2, 1, 0, false, false, false, 226)
 MXK_PW_X2(mx_pw_ch2_k4_f, CH, 2, 4, 0, false, false, false, 226)
+MXK_PW_X2(mx_pw_ch2_k4_ln2_f, CH, 2, 4, 2, false, false, false, 72)
+// the unfused split-reduction kernel (a GEMM with no epilogue), paired
+extern "C" __global__ __launch_bounds__(256) void mx_pw_ch2_k4_x2(DualGemmArgs d) {
+    if (blockIdx.x < d.na)
+        pw::body<pw::CH, 2, 4, false, 0, false, false>(d.a, blockIdx.x, d.na, 0);
+    else
+        pw::body<pw::CH, 2, 4, false, 0, false, false>(d.b, blockIdx.x - d.na, gridDim.x - d.na, 0);
+}
