@@ -11,7 +11,9 @@ import os
 import numpy as np
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_DIR = os.path.join(os.path.dirname(_HERE), "lib")
+# MAXIM_LIB_DIR: another build of the libraries (e.g. lib-san, the host
+# code under the address and undefined-behaviour sanitizers)
+LIB_DIR = os.environ.get("MAXIM_LIB_DIR") or os.path.join(os.path.dirname(_HERE), "lib")
 
 OP_NAMES = [
     "copy", "add", "mul", "gate_apply", "gelu", "lrelu", "sigmoid", "chan_ln",
