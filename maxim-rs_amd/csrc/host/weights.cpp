@@ -75,6 +75,7 @@ struct JVal {
 
 struct JParser {
     const char *p, *e;
+    int depth = 0;  // nesting, bounded so a hostile header cannot exhaust the stack
     void ws() { while (p < e && (*p == ' ' || *p == '\n' || *p == '\r' || *p == '\t')) ++p; }
     [[noreturn]] void fail(const char *what) {
         throw Error(std::string("safetensors header: ") + what);
@@ -114,6 +115,12 @@ struct JParser {
         return s;
     }
     JVal value() {
+        if (++depth > 64) fail("nested too deeply");
+        JVal v = item();
+        --depth;
+        return v;
+    }
+    JVal item() {
         ws();
         if (p >= e) fail("unexpected end");
         JVal v;
@@ -253,35 +260,49 @@ Weights *Weights::open(const std::string &path) {
             const JVal *dt = t.find("dtype"), *sh = t.find("shape"), *off = t.find("data_offsets");
             if (!dt || !sh || !off || off->arr.size() != 2)
                 throw Error(path + ": tensor " + kv.first + " has an incomplete entry");
+            // Sizes and offsets are whole non-negative numbers, the element
+            // count does not overflow, and the byte count is checked before
+            // anything is allocated: a header cannot make the reader allocate
+            // more than the file holds.
+            auto whole = [&](const JVal &v, const char *what) -> uint64_t {
+                if (v.kind != JVal::Num || !(v.num >= 0.0) || v.num > 9.0e15 || v.num != (double)(uint64_t)v.num)
+                    throw Error(path + ": tensor " + kv.first + " has a bad " + what);
+                return (uint64_t)v.num;
+            };
+            if (sh->kind != JVal::Arr || off->kind != JVal::Arr)
+                throw Error(path + ": tensor " + kv.first + " has an incomplete entry");
             Tensor ten;
             uint64_t n = 1;
-            for (auto &d : sh->arr) { ten.shape.push_back((int64_t)d.num); n *= (uint64_t)d.num; }
-            uint64_t a = (uint64_t)off->arr[0].num, b = (uint64_t)off->arr[1].num;
+            for (auto &d : sh->arr) {
+                const uint64_t k = whole(d, "shape");
+                ten.shape.push_back((int64_t)k);
+                if (__builtin_mul_overflow(n, k, &n)) throw Error(path + ": tensor " + kv.first + " is too large");
+            }
+            const uint64_t a = whole(off->arr[0], "data offset"), b = whole(off->arr[1], "data offset");
             if (b < a || base + b > fsize) throw Error(path + ": tensor " + kv.first + " runs past the file");
+            const uint64_t esz = dt->str == "F32" ? 4 : dt->str == "F16" || dt->str == "BF16" ? 2 : dt->str == "F64" ? 8 : 0;
+            if (!esz) throw Error(path + ": " + kv.first + " has unsupported dtype " + dt->str);
+            if (n > (b - a) / esz || b - a != n * esz) throw Error(path + ": " + kv.first + " has the wrong byte count");
             std::vector<char> raw(b - a);
             f.seekg(base + a);
             f.read(raw.data(), b - a);
+            if (!f) throw Error(path + ": tensor " + kv.first + " could not be read");
             ten.data.resize(n);
             if (dt->str == "F32") {
-                if (b - a != n * 4) throw Error(path + ": " + kv.first + " has the wrong byte count");
                 memcpy(ten.data.data(), raw.data(), n * 4);
             } else if (dt->str == "F16" || dt->str == "BF16") {
-                if (b - a != n * 2) throw Error(path + ": " + kv.first + " has the wrong byte count");
                 for (uint64_t i = 0; i < n; ++i) {
                     uint16_t h;
                     memcpy(&h, raw.data() + 2 * i, 2);
                     if (dt->str == "F16") ten.data[i] = half_to_float(h);
                     else { uint32_t u = (uint32_t)h << 16; memcpy(&ten.data[i], &u, 4); }
                 }
-            } else if (dt->str == "F64") {
-                if (b - a != n * 8) throw Error(path + ": " + kv.first + " has the wrong byte count");
+            } else {
                 for (uint64_t i = 0; i < n; ++i) {
                     double d;
                     memcpy(&d, raw.data() + 8 * i, 8);
                     ten.data[i] = (float)d;
                 }
-            } else {
-                throw Error(path + ": " + kv.first + " has unsupported dtype " + dt->str);
             }
             w->tensors.emplace(kv.first, std::move(ten));
         }
