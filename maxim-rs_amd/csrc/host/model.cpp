@@ -643,6 +643,13 @@ Plan *Builder::build(int64_t h, int64_t wd) {
     const int depth = cfg_.depth, stages = cfg_.num_stages, nss = cfg_.num_supervision_scales;
     const int64_t features = cfg_.features;
     if (h <= 0 || wd <= 0) throw Error("the plan needs a positive input size");
+    // Every buffer's element count (at most 16 x features channels times the
+    // input plane) and every offset of the packed arena must stay far inside
+    // 64 bits; 2^24 per side is 256 TB per full-resolution tensor, far beyond
+    // any device or host, which refuse long before.
+    if (h > (int64_t)1 << 24 || wd > (int64_t)1 << 24)
+        throw Error("the plan's input is " + std::to_string(wd) + "x" + std::to_string(h) +
+                    "; each side is limited to 16777216 pixels");
 
     int64_t input = buf(3, h, wd, "input");
     rec("input", input);

@@ -233,3 +233,18 @@ def test_graph_wiring_matches_the_reference_transcription(case):
         got = buf(plan, arena, names[k]).reshape(ref.shape)
         err = float(np.abs(got.astype(np.float64) - ref).max())
         assert err <= 1e-5 * float(np.abs(ref).max()), (k, err)
+
+
+def test_input_sides_beyond_the_limit_are_refused():
+    """A side over 2^24 pixels is refused by name (past it, buffer sizes and
+    arena offsets would overflow 64 bits and wrap to a small arena); at the
+    limit every size is still exact: the arena holds the largest buffer."""
+    from maxim_amd import plan as P
+    w = weights("S-2")
+    for h, wd in [(64, (1 << 24) + 64), ((1 << 40), (1 << 40)), ((1 << 62), (1 << 62))]:
+        with pytest.raises(P.MaximError, match="limited to 16777216"):
+            P.Plan(w, h, wd)
+    p = P.Plan(P.Weights.synthetic("M-3", seed=1), 1 << 24, 1 << 24)
+    largest = max(c * h * ww for c, h, ww in p.bufs)
+    assert largest >= 64 * (1 << 48)  # the full-resolution features, 64 channels of 2^48 pixels
+    assert p.arena_len >= largest and p.arena_len * 4 < (1 << 64)
