@@ -161,3 +161,30 @@ def test_program_walk_names_the_step_of_a_wrong_op(gpu_ok):
 
     r = D.verify_program_walk(plan, smooth_image(64, 64, seed=6), planted)
     assert r["bad"] >= 1 and r["failures"][0]["ops"] == (a, b), (a, b, r["failures"][:2])
+
+
+@pytest.mark.parametrize("variant,h,w", [("S-1", 128, 192), ("M-1", 128, 128), ("M-2", 64, 128), ("M-3", 128, 64)])
+def test_every_variant_step_by_step(gpu_ok, variant, h, w):
+    """The variants the reference's Config supports beyond the benchmarked
+    S-2 / S-3 (src/config.rs:33-56): one stage (S-1) and the 64-feature
+    models (M-1..M-3, whose levels carry 64 to 512 channels and so take other
+    tile widths, band LayerNorms and conv forms): the fused program step by
+    step on the CPU path's inputs at the GEMM bar, and the whole pass against
+    the CPU path at the north-star bar."""
+    from conftest import psnr, run_oracle
+    from maxim_amd import hip as H
+    from maxim_amd import plan as P
+    plan = P.Plan(weights(variant), h, w)
+    img = smooth_image(h, w, seed=17)
+    r = program_walk(plan, img)
+    print("worst by kernel", sorted(r["worst_by_kernel"].items(), key=lambda kv: -kv[1])[:6])
+    assert r["bad"] == 0, r["failures"][:5]
+    gpu = H.Gpu(plan)
+    got = gpu.run(img)
+    gpu.close()
+    arena = run_oracle(plan, img)
+    o = int(plan.offs[plan.output])
+    want = arena[o:o + got.size].reshape(got.shape)
+    err = float(np.abs(got.astype(np.float64) - want).max())
+    print("%s %dx%d: %d ops, whole pass max-abs %.3g, PSNR %.1f dB" % (variant, w, h, len(plan.ops), err, psnr(got, want)))
+    assert err <= 2e-3 and psnr(got, want) >= 50.0
