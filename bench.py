@@ -39,7 +39,7 @@ in HBM when the timed region starts. Prints ONE JSON line:
                 pass, bit for bit, and against the CPU path (max-abs, PSNR);
                 the run fails if they disagree
 
-  python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-c5]
+  python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-c5] [--variant S-3]
 """
 
 import argparse
@@ -93,6 +93,8 @@ def main():
                          "(the same kernels; for tracing tools)")
     ap.add_argument("--no-c5", action="store_true", help="skip the 4096x4096 leg")
     ap.add_argument("--cpu-threads", type=int, default=host_threads())
+    ap.add_argument("--variant", default="S-3", choices=["S-1", "S-2", "S-3", "M-1", "M-2", "M-3"],
+                    help="the model (default S-3, the configuration the metric is quoted on)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build runs on one GPU only (a MAXIM pass is one image on one device; "
@@ -103,13 +105,14 @@ def main():
     from maxim_amd import hip as H
     from maxim_amd import roofline as R
 
-    w = P.Weights.synthetic("S-3", seed=SEED, gain=GAIN, bias_std=0.02, ln_std=0.1)
+    name = model_name(args.variant)
+    w = P.Weights.synthetic(args.variant, seed=SEED, gain=GAIN, bias_std=0.02, ln_std=0.1)
     raw = smooth_image(400, 600, seed=4)
     pad = P.preprocess(raw, 64)
     _, ph, pw = pad.img.shape
     plan = P.Plan(w, ph, pw)
     n_ops = len(plan.ops)
-    print("bench: MAXIM-3S %dx%d, %d ops, arena %.1f MiB" % (pw, ph, n_ops, plan.arena_bytes / 2**20),
+    print("bench: %s %dx%d, %d ops, arena %.1f MiB" % (name, pw, ph, n_ops, plan.arena_bytes / 2**20),
           file=sys.stderr, flush=True)
 
     gpu = H.Gpu(plan)
@@ -244,16 +247,16 @@ def main():
     validation = {"replay_equals_first_pass": same}
     cpu = None
     if not args.no_cpu:
-        cpu, ref = cpu_baseline(plan, pad.img, args.cpu_threads)
+        cpu, ref = cpu_baseline(plan, pad.img, args.cpu_threads, name)
         err = float(np.abs(out_last.astype(np.float64) - ref).max())
         mse = float(((np.clip(out_last, 0, 1) - np.clip(ref, 0, 1)).astype(np.float64) ** 2).mean())
         validation["max_abs_vs_cpu"] = err
         validation["psnr_db_vs_cpu"] = 10 * np.log10(1.0 / mse) if mse > 0 else float("inf")
     gpu.close()
-    c5 = None if args.no_c5 else c5_leg(w, R)
+    c5 = None if args.no_c5 else c5_leg(w, R, name)
 
     line = {
-        "metric": METRIC,
+        "metric": METRIC.replace("MAXIM-3S", name),
         "value": 1e3 / ms_per_step,
         "unit": "images/s",
         "n_gpus": 1,
@@ -265,8 +268,8 @@ def main():
         "vs_baseline": None,
         "dtype": "fp32",
         "data": "synthetic: seeded He-normal x0.3 weights, 600x400 smooth pattern + N(0,0.1) image",
-        "config": {"workload": "C4: MAXIM-3S, 600x400 RGB reflect-padded to 640x448, one image per step",
-                   "variant": "S-3", "ops": n_ops, "launch": "eager" if args.eager else "graph",
+        "config": {"workload": "C4: %s, 600x400 RGB reflect-padded to 640x448, one image per step" % name,
+                   "variant": args.variant, "ops": n_ops, "launch": "eager" if args.eager else "graph",
                    "arena_mib": round(plan.arena_bytes / 2**20, 1),
                    "device_arena_mib": round(dev_arena / 2**20, 1),
                    "gflop_per_image": round(fl_all / 1e9, 1), "gb_per_image": round(by_all / 1e9, 2),
@@ -291,6 +294,11 @@ def main():
         sys.exit(1)
 
 
+def model_name(variant):
+    """S-3 -> MAXIM-3S, M-2 -> MAXIM-2M: the reference's names for the variants."""
+    return "MAXIM-%s%s" % (variant[2], variant[0])
+
+
 def host_threads():
     """The host cores this process may use (OMP_NUM_THREADS when the host
     sets it, as the GPU boxes do, else every core)."""
@@ -310,7 +318,7 @@ def cpu_model():
     return "unknown"
 
 
-def c5_leg(w, R, steps=3):
+def c5_leg(w, R, name, steps=3):
     """C5: MAXIM-3S on a 4096x4096 image (uniform [0, 1) plus N(0, 0.05),
     clipped), the same weights: ms/image over graph replays, the dominant
     kernel's rate (its tensors are far larger than the Infinity Cache, so its
@@ -364,7 +372,7 @@ def c5_leg(w, R, steps=3):
         mem = [r for r in rows if r["bound"] == "hbm"]
         gemm = [r for r in rows if r["bound"] == "mfma"][:8]
         bound_ms = sum(launch_bound_ms(c[0], c[1], R) for c in cost)
-        res = {"workload": "C5: MAXIM-3S, 4096x4096 RGB, one image per step", "ms_per_image": ms,
+        res = {"workload": "C5: %s, 4096x4096 RGB, one image per step" % name, "ms_per_image": ms,
                "images_per_s": 1e3 / ms, "steps": steps, "arena_gib": round(plan.arena_bytes / 2**30, 2),
                "kernel_ms_per_pass": tot, "tflops_effective": fl_all / (ms * 1e-3) / 1e12,
                "tb_per_s_effective": by_all / (ms * 1e-3) / 1e12,
@@ -524,7 +532,7 @@ def launch_costs(plan, steps, launches, R, spans=None):
     return out
 
 
-def cpu_baseline(plan, img, threads):
+def cpu_baseline(plan, img, threads, name="MAXIM-3S"):
     """The CPU path (oracle/: a C restatement of src/exec_cpu.rs, OpenMP over
     channels, rows and pixels) on this host: the median of three full C4
     passes on `threads` cores, and one single-thread C1 pass (MAXIM-2S,
@@ -565,8 +573,8 @@ def cpu_baseline(plan, img, threads):
     print("bench: CPU C4 %s s on %d threads, C1 %.1f s and C2 %.2f s on 1 thread (%s)"
           % (", ".join("%.2f" % t for t in times), used, dt1, dt2, cpu_model()), file=sys.stderr, flush=True)
     rec = {"value": 1.0 / med, "unit": "images/s", "cores": used, "kind": "port",
-           "sample": "median of 3 full MAXIM-3S 640x448 passes (2885 ops) of the C restatement of "
-                     "src/exec_cpu.rs: %s s" % ", ".join("%.2f" % t for t in times),
+           "sample": "median of 3 full %s 640x448 passes (%d ops) of the C restatement of src/exec_cpu.rs: %s s"
+                     % (name, len(plan.ops), ", ".join("%.2f" % t for t in times)),
            "cpu_model": cpu_model(), "host_cores_visible": os.cpu_count(),
            "c1_single_thread": {"seconds": dt1, "images_per_s": 1.0 / dt1,
                                 "workload": "C1: MAXIM-2S 256x256, one pass, 1 thread"},
