@@ -749,13 +749,15 @@ private:
         static const char *names[2][3] = {{"mx_pw_ch1", "mx_pw_ch2", "mx_pw_ch4"},
                                           {"mx_pw_rw1", "mx_pw_rw2", "mx_pw_rw4"}};
         // Tile width and reduction split, from measurements on MI355X: 32
-        // weight outputs per wave, except the row-major form's long (K >=
-        // 256) reductions, which reuse each operand load over 64 (the
-        // channel-major form is 3-12% faster at 32 there too: 1x1 convs of
-        // 256-512 inputs, GateMm over 256 tokens); the block's four waves
-        // split reductions of 128 and more, and shorter ones when one wave
-        // per tile would leave SIMDs idle.
-        const int ti = wout <= 16 ? 0 : (wout <= 32 || a.K < 256 || layout == 0) ? 1 : 2, tmw = 1 << ti;
+        // weight outputs per wave in both layouts (64 for the row-major
+        // form's long reductions reused each operand load twice as often
+        // but held 186 VGPRs, two waves per SIMD: the GateMm mode-1 launches
+        // run 2-7% faster at 32 at 224x320 and the same at 448x640; the
+        // channel-major form is 3-12% faster at 32 for 1x1 convs of 256-512
+        // inputs and GateMm over 256 tokens); the block's four waves split
+        // reductions of 128 and more, and shorter ones when one wave per
+        // tile would leave SIMDs idle.
+        const int ti = wout <= 16 ? 0 : 1, tmw = 1 << ti;
         const int64_t nib = (wout + 16 * tmw - 1) / (16 * tmw);
         const int64_t tiles = nib * ((slen + 63) / 64);
         if (tiles > 0x7fffffffLL) return false;
