@@ -2917,6 +2917,11 @@ void Gpu::pair_launches(const mx_plan_desc *p) {
         fns_[n] = f;
         return f;
     };
+    // a kernel pairing two different launches: A__B_x2, A's blocks first
+    auto hx2fn = [&](const char *a, const char *b) -> hipFunction_t {
+        if (strncmp(b, "mx_pw_", 6)) return nullptr;
+        return x2fn((std::string(a) + "__" + (b + 6)).c_str());
+    };
     auto single = [&](const Step &st) {
         if (st.launches.size() != 1 || st.launches[0].kind != 1) return false;
         const char *n = st.launches[0].name;
@@ -3020,11 +3025,22 @@ void Gpu::pair_launches(const mx_plan_desc *p) {
             const Launch &l = prog[node[u]].launches[0];
             return l.g[1] == 1 && l.g[2] == 1 && l.g[0] <= (unsigned)(5 * cus);
         };
+        // the kernel running u and v in one grid (same kernel: its _x2 form;
+        // two kernels: A__B_x2, with `swap` when v's blocks come first)
+        auto pairfn = [&](size_t u, size_t v, bool &swap) -> hipFunction_t {
+            swap = false;
+            if (kname(u) == kname(v)) return x2fn(kname(u));
+            if (std::getenv("MAXIM_NO_HPAIR")) return nullptr;
+            if (hipFunction_t f = hx2fn(kname(u), kname(v))) return f;
+            swap = true;
+            return hx2fn(kname(v), kname(u));
+        };
         auto can_pair = [&](size_t u, size_t v) {
-            const bool ok = kname(u) == kname(v) && one(u) && one(v) && !(reach[v] >> u & 1) && !(reach[u] >> v & 1);
-            if (ok && !x2fn(kname(u)) && std::getenv("MAXIM_PAIR_LOG"))
+            const bool ok = one(u) && one(v) && !(reach[v] >> u & 1) && !(reach[u] >> v & 1);
+            bool swap;
+            if (ok && kname(u) == kname(v) && !x2fn(kname(u)) && std::getenv("MAXIM_PAIR_LOG"))
                 fprintf(stderr, "maxim: no paired form of %s\n", kname(u));
-            return ok && x2fn(kname(u)) != nullptr;
+            return ok && pairfn(u, v, swap) != nullptr;
         };
         // list scheduling: entries are (u) or (u, v)
         std::vector<std::pair<int, int>> seq;
@@ -3075,20 +3091,23 @@ void Gpu::pair_launches(const mx_plan_desc *p) {
                 st.launches.back().span[1] = sa.last;
                 continue;
             }
-            const Step &sb = prog[node[e.second]];
-            const Launch &b = sb.launches[0];
-            Launch d = a;
-            d.span[0] = sa.first;
-            d.span[1] = sa.last;
-            d.span[2] = sb.first;
-            d.span[3] = sb.last;
-            d.name = intern(std::string(a.name) + "_x2");
-            d.f = x2fn(a.name);
+            bool swap = false;
+            const hipFunction_t pf = pairfn((size_t)e.first, (size_t)e.second, swap);
+            const Step &s0 = prog[node[swap ? e.second : e.first]], &s1 = prog[node[swap ? e.first : e.second]];
+            const Launch &l0 = s0.launches[0], &l1 = s1.launches[0];
+            Launch d = l0;
+            d.span[0] = s0.first;
+            d.span[1] = s0.last;
+            d.span[2] = s1.first;
+            d.span[3] = s1.last;
+            d.name = intern(l0.name == l1.name ? std::string(l0.name) + "_x2"
+                                               : std::string(l0.name) + "__" + (l1.name + 6) + "_x2");
+            d.f = pf;
             DualGemmArgs da{};
-            memcpy(&da.a, a.a0, sizeof(GemmArgs));
-            memcpy(&da.b, b.a0, sizeof(GemmArgs));
-            da.na = a.g[0];
-            d.g[0] = a.g[0] + b.g[0];
+            memcpy(&da.a, l0.a0, sizeof(GemmArgs));
+            memcpy(&da.b, l1.a0, sizeof(GemmArgs));
+            da.na = l0.g[0];
+            d.g[0] = l0.g[0] + l1.g[0];
             d.kind = 3;
             set_args(d, da);
             st.main = st.launches.size();

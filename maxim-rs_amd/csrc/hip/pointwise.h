@@ -79,9 +79,11 @@ enum { EP_U = 1, EP_R1 = 2, EP_R2 = 4, EP_GELU = 8, EP_LRELU = 16, EP_YMAP = 32,
 // waves in turn), so its normalised X differs from theirs by rounding.
 // (ux, nx): this block's index and the block count along x, by: the batch;
 // a kernel pairing two launches in one grid passes each part its own.
+// XR: the split reduction's LDS buffer comes from the caller (xred, 4 x 16
+// TMW x 64 floats), so two different instances in one kernel share one.
 template <int LAYOUT, int TMW, int KS, bool FUSED, int LN, bool XM = false, bool XMUL = false, bool CT = false,
-          bool LNO = false, int EP = -1, bool FOLD = false>
-__device__ void body(const GemmArgs &a, int ux, int nx, int by) {
+          bool LNO = false, int EP = -1, bool FOLD = false, bool XR = false>
+__device__ void body(const GemmArgs &a, int ux, int nx, int by, float *xred = nullptr) {
     const bool has_u = EP < 0 ? a.e.u != nullptr : (EP & EP_U) != 0;
     const bool has_r1 = EP < 0 ? a.e.r1 != nullptr : (EP & EP_R1) != 0;
     const bool has_r2 = EP < 0 ? a.e.r2 != nullptr : (EP & EP_R2) != 0;
@@ -392,7 +394,8 @@ __device__ void body(const GemmArgs &a, int ux, int nx, int by) {
     }
     if (s < nSw) mma(xb, wb, lb, mb, false);
 
-    __shared__ float red[KS == 1 ? 1 : 4 * NACC * 64];
+    __shared__ float red_own[KS == 1 || XR ? 1 : 4 * NACC * 64];
+    float *const red = XR ? xred : red_own;
     if (KS == 4) {
 #pragma unroll
         for (int j = 0; j < 4; ++j)
@@ -787,6 +790,27 @@ MXK_PW_X2(mx_pw_ch1_f, CH, 1, 1, 0, false, false, false, 226)
 MXK_PW_X2(mx_pw_ch2_f, CH, 2, 1, 0, false, false, false, 226)
 MXK_PW_X2(mx_pw_ch2_k4_f, CH, 2, 4, 0, false, false, false, 226)
 MXK_PW_X2(mx_pw_ch2_k4_ln2_f, CH, 2, 4, 2, false, false, false, 72)
+// A__B_x2: two different split-reduction GEMMs, independent of each other,
+// side by side in one grid (the first d.na blocks run A, the rest B) with one
+// reduction buffer for both (each instance would otherwise bring its own and
+// halve the blocks per CU): the grid and block branches' GateMms of a
+// multi-axis gMLP block, mode 0 over a folded batch and mode 1.
+extern "C" __global__ __launch_bounds__(256) void mx_pw_chb2_k4_xm__rw2_k4_xm_x2(DualGemmArgs d) {
+    __shared__ float red[4 * 32 * 64];
+    if (blockIdx.x < d.na)
+        pw::body<pw::CH, 2, 4, false, 0, true, false, false, false, -1, true, true>(d.a, blockIdx.x, d.na, 0, red);
+    else
+        pw::body<pw::RW, 2, 4, false, 0, true, false, false, false, -1, false, true>(d.b, blockIdx.x - d.na,
+                                                                                      gridDim.x - d.na, 0, red);
+}
+extern "C" __global__ __launch_bounds__(256) void mx_pw_chb2_k4_f_e65__rw2_k4_f_e65_x2(DualGemmArgs d) {
+    __shared__ float red[4 * 32 * 64];
+    if (blockIdx.x < d.na)
+        pw::body<pw::CH, 2, 4, true, 0, false, false, false, false, 65, true, true>(d.a, blockIdx.x, d.na, 0, red);
+    else
+        pw::body<pw::RW, 2, 4, true, 0, false, false, false, false, 65, false, true>(d.b, blockIdx.x - d.na,
+                                                                                      gridDim.x - d.na, 0, red);
+}
 // the unfused split-reduction kernel (a GEMM with no epilogue), paired
 extern "C" __global__ __launch_bounds__(256) void mx_pw_ch2_k4_x2(DualGemmArgs d) {
     if (blockIdx.x < d.na)
