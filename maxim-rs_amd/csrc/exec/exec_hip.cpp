@@ -2892,12 +2892,14 @@ void Gpu::build_program(const mx_plan_desc *p) {
 // steps of each other (the grid and block branches of a multi-axis gMLP
 // block: their in-projections, their out-projections) become one launch of
 // the kernel's _x2 form, so that two grids too small to fill the chip share
-// it and one tail. Within a window of consecutive steps whose launches are
-// all single streaming GEMMs (or none), launches are list-scheduled over the
-// steps' dependencies - any two steps whose device bytes (arena, and the
-// scratch statistics their arguments name) overlap with a write keep their
-// order - taking two ready launches of one kernel together where it can, and
-// otherwise holding back a launch whose partner is still waiting on others.
+// it and one tail. Within a window of consecutive steps with one launch each
+// (or none), launches are list-scheduled over the steps' dependencies - any
+// two steps whose device bytes (arena, and the scratch statistics their
+// arguments name) overlap with a write keep their order - taking two ready
+// launches of one kernel together where it can, and otherwise holding back a
+// launch whose partner is still waiting on others. Only streaming GEMMs pair;
+// the other kernels of a window (LayerNorms, permutations, the general GEMM
+// at shapes the streaming one does not take) keep their place among them.
 // A window in which anything was paired becomes one step over all its ops:
 // every op still computes exactly what it did, in a dependency-respecting
 // order, so results are unchanged to the bit; a run of ops that cuts the
@@ -2928,15 +2930,36 @@ void Gpu::pair_launches(const mx_plan_desc *p) {
         const size_t k = strlen(n);
         return strncmp(n, "mx_pw_", 6) == 0 && !(k > 2 && strcmp(n + k - 2, "_t") == 0);
     };
-    auto member = [&](const Step &st) { return (st.launches.empty() && st.pre.empty()) || single(st); };
+    // Any other kernel of a window never pairs; its bytes are taken from its
+    // ops (sources read, destinations read and written, the step's fused
+    // operands read and written, and all of the scratch both ways), a
+    // superset of what it touches. A step of a streaming GEMM followed by the
+    // LayerNorm of its output band (a LayerNorm kernel of its own, where the
+    // band is wider than the GEMM's epilogue takes) gives two nodes, the
+    // GEMM's ops and then the LayerNorm op.
+    const bool specs_ok = pg.specs.size() == prog.size();
+    auto is_pw = [&](const Launch &l) {
+        const size_t k = strlen(l.name);
+        return l.kind == 1 && strncmp(l.name, "mx_pw_", 6) == 0 && !(k > 2 && strcmp(l.name + k - 2, "_t") == 0);
+    };
+    auto other = [&](const Step &st) {
+        return specs_ok && st.launches.size() == 1 && st.pre.empty() && st.launches[0].kind != 3 && !single(st);
+    };
+    auto banded = [&](const Step &st) {
+        return specs_ok && st.launches.size() == 2 && st.pre.empty() && st.last - st.first >= 2 &&
+               is_pw(st.launches[0]) && strncmp(st.launches[1].name, "mx_chan_ln_c", 12) == 0 &&
+               p->ops[st.last - 1].kind == MX_OP_CHAN_LN;
+    };
+    auto member = [&](const Step &st) {
+        return (st.launches.empty() && st.pre.empty()) || single(st) || other(st) || banded(st);
+    };
     // the device memory a step's streaming-GEMM launch reads and writes,
     // from its arguments: X (and a folded Mul's second factor), the epilogue
     // operands and the folded LayerNorm's statistics are read; the output and
     // the output LayerNorm's band (or statistics) are written. Extents are
     // per batch (a block map permutes within them: X over its plane, Y
     // within M x N); weights and biases are never written and are left out.
-    auto footprint = [&](const Step &st, std::vector<Iv> &rd, std::vector<Iv> &wr) {
-        const Launch &l = st.launches[0];
+    auto footprint = [&](const Launch &l, std::vector<Iv> &rd, std::vector<Iv> &wr) {
         GemmArgs a;
         memcpy(&a, l.a0, sizeof a);
         auto add = [&](std::vector<Iv> &v, const float *q, int64_t stride, uint64_t len) {
@@ -2965,6 +2988,23 @@ void Gpu::pair_launches(const mx_plan_desc *p) {
             else
                 add(wr, a.lo.y, 0, (uint64_t)(a.M - a.lo.row0) * (uint64_t)a.N);
         }
+    };
+    auto footprint_ops = [&](size_t k, uint64_t first, uint64_t last, std::vector<Iv> &rd, std::vector<Iv> &wr) {
+        auto buf = [&](int64_t b, bool w) {
+            if (b < 0) return;
+            const uint64_t n = (uint64_t)(p->bufs[b].c * p->bufs[b].h * p->bufs[b].w);
+            rd.push_back(Iv{0, doff[b], doff[b] + n});
+            if (w) wr.push_back(Iv{0, doff[b], doff[b] + n});
+        };
+        for (uint64_t o = first; o < last; ++o) {
+            buf(p->ops[o].src, false);
+            buf(p->ops[o].src2, false);
+            buf(p->ops[o].dst, true);
+        }
+        const StepSpec &sp = pg.specs[k];
+        for (int64_t b : {sp.out, sp.u, sp.r1, sp.r2, sp.m, sp.xsrc, sp.r1p, sp.pout}) buf(b, true);
+        rd.push_back(Iv{1, 0, scratch_len});
+        wr.push_back(Iv{1, 0, scratch_len});
     };
     auto meets = [](const std::vector<Iv> &x, const std::vector<Iv> &y) {
         for (const Iv &u : x)
@@ -3000,33 +3040,57 @@ void Gpu::pair_launches(const mx_plan_desc *p) {
             i = j;
             continue;
         }
-        std::vector<size_t> node;  // window steps with a launch
-        for (size_t k = i; k < j; ++k)
-            if (!prog[k].launches.empty()) node.push_back(k);
+        // window nodes: each launch of its steps, with the ops it computes
+        std::vector<size_t> node;  // its step
+        std::vector<const Launch *> ln;
+        std::vector<std::array<uint64_t, 2>> spn;
+        for (size_t k = i; k < j; ++k) {
+            const Step &s = prog[k];
+            for (size_t q = 0; q < s.launches.size(); ++q) {
+                node.push_back(k);
+                ln.push_back(&s.launches[q]);
+                if (s.launches.size() == 1)
+                    spn.push_back({s.first, s.last});
+                else
+                    spn.push_back(q == 0 ? std::array<uint64_t, 2>{s.first, s.last - 1}
+                                         : std::array<uint64_t, 2>{s.last - 1, s.last});
+            }
+        }
         const size_t m = node.size();
+        if (m > 32) {
+            for (size_t k = i; k < j; ++k) out.push_back(std::move(prog[k]));
+            i = j;
+            continue;
+        }
         std::vector<std::vector<Iv>> rd(m), wr(m);
-        for (size_t u = 0; u < m; ++u) footprint(prog[node[u]], rd[u], wr[u]);
+        for (size_t u = 0; u < m; ++u) {
+            if (is_pw(*ln[u]))
+                footprint(*ln[u], rd[u], wr[u]);
+            else
+                footprint_ops(node[u], spn[u][0], spn[u][1], rd[u], wr[u]);
+        }
         std::vector<uint32_t> pred(m, 0), reach(m, 0);
         for (size_t v = 0; v < m; ++v)
             for (size_t u = 0; u < v; ++u)
-                if (meets(wr[u], rd[v]) || meets(wr[u], wr[v]) || meets(rd[u], wr[v])) pred[v] |= 1u << u;
+                if (node[u] == node[v] || meets(wr[u], rd[v]) || meets(wr[u], wr[v]) || meets(rd[u], wr[v]))
+                    pred[v] |= 1u << u;
         for (size_t v = 0; v < m; ++v) {
             reach[v] = pred[v];
             for (size_t u = 0; u < v; ++u)
                 if (pred[v] >> u & 1) reach[v] |= reach[u];
         }
-        auto kname = [&](size_t u) { return prog[node[u]].launches[0].name; };
+        auto kname = [&](size_t u) { return ln[u]->name; };
         if (std::getenv("MAXIM_PAIR_LOG") && m > 1) {
             fprintf(stderr, "maxim: window steps [%zu, %zu):", i, j);
-            for (size_t u = 0; u < m; ++u) fprintf(stderr, " %zu:%s(g%u/%u, pred %x)", node[u], kname(u), prog[node[u]].launches[0].g[0], prog[node[u]].launches[0].g[1], pred[u]);
+            for (size_t u = 0; u < m; ++u) fprintf(stderr, " %zu:%s(g%u/%u, pred %x)", node[u], kname(u), ln[u]->g[0], ln[u]->g[1], pred[u]);
             fprintf(stderr, "\n");
         }
         // one batch, and a grid of at most ten blocks per CU: a few rounds of
         // blocks, whose ragged last round a partner's blocks fill (with the
         // 224x320 GateMms paired too, C4 measured 23.06 -> 23.00 ms/image)
         auto one = [&](size_t u) {
-            const Launch &l = prog[node[u]].launches[0];
-            return l.g[1] == 1 && l.g[2] == 1 && l.g[0] <= (unsigned)(10 * cus);
+            const Launch &l = *ln[u];
+            return is_pw(l) && l.g[1] == 1 && l.g[2] == 1 && l.g[0] <= (unsigned)(10 * cus);
         };
         // the kernel running u and v in one grid (same kernel: its _x2 form;
         // two kernels: A__B_x2, with `swap` when v's blocks come first)
@@ -3086,23 +3150,21 @@ void Gpu::pair_launches(const mx_plan_desc *p) {
         for (size_t k = i; k < j; ++k)
             for (Launch &l : prog[k].pre) st.pre.push_back(l);
         for (auto &e : seq) {
-            const Step &sa = prog[node[e.first]];
-            const Launch &a = sa.launches[0];
             if (e.second < 0) {
-                st.launches.push_back(a);
-                st.launches.back().span[0] = sa.first;
-                st.launches.back().span[1] = sa.last;
+                st.launches.push_back(*ln[e.first]);
+                st.launches.back().span[0] = spn[e.first][0];
+                st.launches.back().span[1] = spn[e.first][1];
                 continue;
             }
             bool swap = false;
             const hipFunction_t pf = pairfn((size_t)e.first, (size_t)e.second, swap);
-            const Step &s0 = prog[node[swap ? e.second : e.first]], &s1 = prog[node[swap ? e.first : e.second]];
-            const Launch &l0 = s0.launches[0], &l1 = s1.launches[0];
+            const size_t u0 = swap ? e.second : e.first, u1 = swap ? e.first : e.second;
+            const Launch &l0 = *ln[u0], &l1 = *ln[u1];
             Launch d = l0;
-            d.span[0] = s0.first;
-            d.span[1] = s0.last;
-            d.span[2] = s1.first;
-            d.span[3] = s1.last;
+            d.span[0] = spn[u0][0];
+            d.span[1] = spn[u0][1];
+            d.span[2] = spn[u1][0];
+            d.span[3] = spn[u1][1];
             d.name = intern(l0.name == l1.name ? std::string(l0.name) + "_x2"
                                                : std::string(l0.name) + "__" + (l1.name + 6) + "_x2");
             d.f = pf;

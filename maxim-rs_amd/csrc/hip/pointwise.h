@@ -811,6 +811,17 @@ extern "C" __global__ __launch_bounds__(256) void mx_pw_chb2_k4_f_e65__rw2_k4_f_
         pw::body<pw::RW, 2, 4, true, 0, false, false, false, false, 65, false, true>(d.b, blockIdx.x - d.na,
                                                                                       gridDim.x - d.na, 0, red);
 }
+// the out-projections of the two branches at the smallest resolutions: a
+// residual add (grid branch), and a residual add into a backward permutation
+// (block branch)
+extern "C" __global__ __launch_bounds__(256) void mx_pw_ch2_k4_f_e66__ch2_k4_f_e226_x2(DualGemmArgs d) {
+    __shared__ float red[4 * 32 * 64];
+    if (blockIdx.x < d.na)
+        pw::body<pw::CH, 2, 4, true, 0, false, false, false, false, 66, false, true>(d.a, blockIdx.x, d.na, 0, red);
+    else
+        pw::body<pw::CH, 2, 4, true, 0, false, false, false, false, 226, false, true>(d.b, blockIdx.x - d.na,
+                                                                                       gridDim.x - d.na, 0, red);
+}
 // the unfused split-reduction kernel (a GEMM with no epilogue), paired
 extern "C" __global__ __launch_bounds__(256) void mx_pw_ch2_k4_x2(DualGemmArgs d) {
     if (blockIdx.x < d.na)
