@@ -86,8 +86,8 @@ struct Launch {
     unsigned g[3] = {1, 1, 1};
     unsigned b[3] = {MXK_BLOCK, 1, 1};
     unsigned shm = 0;  // dynamic LDS bytes
-    alignas(16) unsigned char a0[1024];
-    alignas(16) unsigned char a1[32];
+    alignas(16) unsigned char a0[1024] = {};
+    alignas(16) unsigned char a1[32] = {};
     int nparams = 1;
     int kind = 0;  // 1: a0 holds GemmArgs (plain epilogue), 2: ConvArgs, 3: DualGemmArgs
     // The ops this launch computes when its step pairs launches of several
@@ -2268,8 +2268,9 @@ void Program::storage(const mx_plan_desc *p, std::vector<int64_t> &base, std::ve
 // made only of 1x1-conv/GateMm steps and the pointwise, LayerNorm,
 // permutation and copy ops fused around them, every pair of steps with the
 // same op sequence and shapes (the two branches' steps differ only in how
-// their pixels are blocked, not in their sizes) whose buffers do not meet
-// with a write; the region runs from the first such step to the last.
+// their pixels are blocked, not in their sizes), or with the same GEMM,
+// whose buffers do not meet with a write; the region runs from the first
+// such step to the last.
 void Program::plan_regions(const mx_plan_desc *p) {
     regions.clear();
     if (!p->alias_parent || !p->alias_delta) return;
@@ -2305,6 +2306,19 @@ void Program::plan_regions(const mx_plan_desc *p) {
         }
         return v;
     };
+    // the step's GEMM alone: two steps whose GEMMs match but whose fused
+    // ops around them differ (one branch's output permutation folded into
+    // the stores, the other's launched apart) pair as two kernels
+    auto gsig = [&](uint64_t s) {
+        std::vector<int64_t> v;
+        for (uint64_t k = specs[s].first; k < specs[s].last; ++k) {
+            const mx_op &o = p->ops[k];
+            if (o.kind != MX_OP_CONV1X1 && o.kind != MX_OP_GATE_MM) continue;
+            v.insert(v.end(), {(int64_t)o.kind, (int64_t)o.mode, o.c_in, o.c_out, o.h * o.wd, o.n, o.c, o.hw});
+            break;
+        }
+        return v;
+    };
     struct Iv { int64_t owner; uint64_t lo, hi; };
     auto touch = [&](uint64_t s, std::vector<Iv> &rd, std::vector<Iv> &wr) {
         auto iv = [&](int64_t b) { return Iv{base[b], delta[b], delta[b] + len(b)}; };
@@ -2336,7 +2350,7 @@ void Program::plan_regions(const mx_plan_desc *p) {
             if (member(u) != 2) continue;
             const auto su = sig(u);
             for (uint64_t v = u + 1; v < j; ++v) {
-                if (member(v) != 2 || sig(v) != su) continue;
+                if (member(v) != 2 || (sig(v) != su && gsig(v) != gsig(u))) continue;
                 const size_t a = u - i, b = v - i;
                 if (meets(wr[a], rd[b]) || meets(wr[b], rd[a])) continue;
                 lo = std::min(lo, u);
@@ -2932,8 +2946,9 @@ void Gpu::pair_launches(const mx_plan_desc *p) {
     };
     // Any other kernel of a window never pairs; its bytes are taken from its
     // ops (sources read, destinations read and written, the step's fused
-    // operands read and written, and all of the scratch both ways), a
-    // superset of what it touches. A step of a streaming GEMM followed by the
+    // operands read and written, and all of the scratch both ways when its
+    // argument block holds any address inside the scratch), a superset of
+    // what it touches. A step of a streaming GEMM followed by the
     // LayerNorm of its output band (a LayerNorm kernel of its own, where the
     // band is wider than the GEMM's epilogue takes) gives two nodes, the
     // GEMM's ops and then the LayerNorm op.
@@ -2989,7 +3004,20 @@ void Gpu::pair_launches(const mx_plan_desc *p) {
                 add(wr, a.lo.y, 0, (uint64_t)(a.M - a.lo.row0) * (uint64_t)a.N);
         }
     };
-    auto footprint_ops = [&](size_t k, uint64_t first, uint64_t last, std::vector<Iv> &rd, std::vector<Iv> &wr) {
+    auto uses_scratch = [&](const Launch &l) {
+        const uintptr_t lo = (uintptr_t)scratch, hi = (uintptr_t)(scratch + scratch_len);
+        auto scan = [&](const unsigned char *b, size_t n) {
+            for (size_t o = 0; o + 8 <= n; o += 8) {
+                uintptr_t v;
+                memcpy(&v, b + o, 8);
+                if (v >= lo && v < hi) return true;
+            }
+            return false;
+        };
+        return scan(l.a0, sizeof l.a0) || scan(l.a1, sizeof l.a1);
+    };
+    auto footprint_ops = [&](size_t k, const Launch &l, uint64_t first, uint64_t last, std::vector<Iv> &rd,
+                             std::vector<Iv> &wr) {
         auto buf = [&](int64_t b, bool w) {
             if (b < 0) return;
             const uint64_t n = (uint64_t)(p->bufs[b].c * p->bufs[b].h * p->bufs[b].w);
@@ -3003,8 +3031,10 @@ void Gpu::pair_launches(const mx_plan_desc *p) {
         }
         const StepSpec &sp = pg.specs[k];
         for (int64_t b : {sp.out, sp.u, sp.r1, sp.r2, sp.m, sp.xsrc, sp.r1p, sp.pout}) buf(b, true);
-        rd.push_back(Iv{1, 0, scratch_len});
-        wr.push_back(Iv{1, 0, scratch_len});
+        if (uses_scratch(l)) {
+            rd.push_back(Iv{1, 0, scratch_len});
+            wr.push_back(Iv{1, 0, scratch_len});
+        }
     };
     auto meets = [](const std::vector<Iv> &x, const std::vector<Iv> &y) {
         for (const Iv &u : x)
@@ -3067,7 +3097,7 @@ void Gpu::pair_launches(const mx_plan_desc *p) {
             if (is_pw(*ln[u]))
                 footprint(*ln[u], rd[u], wr[u]);
             else
-                footprint_ops(node[u], spn[u][0], spn[u][1], rd[u], wr[u]);
+                footprint_ops(node[u], *ln[u], spn[u][0], spn[u][1], rd[u], wr[u]);
         }
         std::vector<uint32_t> pred(m, 0), reach(m, 0);
         for (size_t v = 0; v < m; ++v)

@@ -211,9 +211,11 @@ def test_gmlp_branches_share_launches(gpu_ok):
     """At C4 the grid and block branches of the multi-axis gMLP blocks below
     full resolution run their in- and out-projections as paired launches
     (one grid for both): each paired launch names two disjoint op ranges
-    inside its step, with the same op sequence, and the pass still equals
-    the unpaired one to the bit (the paired steps' ops run in another order
-    only where nothing they touch overlaps)."""
+    inside its step, with the same GEMM (the ops fused around it may differ:
+    one branch's output permutation folded into the stores, the other's
+    launched apart), and the pass still equals the unpaired one to the bit
+    (the paired steps' ops run in another order only where nothing they
+    touch overlaps)."""
     import os
     from maxim_amd import plan as P
     from maxim_amd import hip as H
@@ -231,8 +233,9 @@ def test_gmlp_branches_share_launches(gpu_ok):
             continue
         pairs += 1
         assert k.endswith("_x2") and a <= r1[0] < r1[1] <= b and (r0[1] <= r1[0] or r1[1] <= r0[0])
-        kinds = lambda r: [(op.kind, op.c_in, op.c_out, op.h * op.wd) for op in plan.ops[r[0]:r[1]]]
-        assert kinds(r0) == kinds(r1)
+        gemm = lambda r: [(op.kind, op.c_in, op.c_out, op.h * op.wd) for op in plan.ops[r[0]:r[1]]
+                          if op.kind in (P.CONV1X1, P.GATE_MM)][:1]
+        assert gemm(r0) == gemm(r1) and gemm(r0), (k, r0, r1)
     gpu.close()
     print("%d paired launches" % pairs)
     assert pairs >= 40
