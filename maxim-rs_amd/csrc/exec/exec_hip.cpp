@@ -89,7 +89,7 @@ struct Launch {
     alignas(16) unsigned char a0[1024] = {};
     alignas(16) unsigned char a1[32] = {};
     int nparams = 1;
-    int kind = 0;  // 1: a0 holds GemmArgs (plain epilogue), 2: ConvArgs, 3: DualGemmArgs
+    int kind = 0;  // 1: a0 holds GemmArgs (plain epilogue), 2: ConvArgs, 3: DualGemmArgs, 4: DualLnArgs
     // The ops this launch computes when its step pairs launches of several
     // former steps: [span[0], span[1]), and for a paired launch also
     // [span[2], span[3]); all zero: the whole step's ops.
@@ -2911,9 +2911,10 @@ void Gpu::build_program(const mx_plan_desc *p) {
 // two steps whose device bytes (arena, and the scratch statistics their
 // arguments name) overlap with a write keep their order - taking two ready
 // launches of one kernel together where it can, and otherwise holding back a
-// launch whose partner is still waiting on others. Only streaming GEMMs pair;
-// the other kernels of a window (LayerNorms, permutations, the general GEMM
-// at shapes the streaming one does not take) keep their place among them.
+// launch whose partner is still waiting on others. Streaming GEMMs and
+// LayerNorms pair; the other kernels of a window (permutations, the general
+// GEMM at shapes the streaming one does not take) keep their place among
+// them.
 // A window in which anything was paired becomes one step over all its ops:
 // every op still computes exactly what it did, in a dependency-respecting
 // order, so results are unchanged to the bit; a run of ops that cuts the
@@ -2957,8 +2958,11 @@ void Gpu::pair_launches(const mx_plan_desc *p) {
         const size_t k = strlen(l.name);
         return l.kind == 1 && strncmp(l.name, "mx_pw_", 6) == 0 && !(k > 2 && strcmp(l.name + k - 2, "_t") == 0);
     };
+    // a LayerNorm launch (its own kernel, not a statistics pass): pairs with
+    // another of the same kernel
+    auto is_ln = [&](const Launch &l) { return l.kind == 0 && strncmp(l.name, "mx_chan_ln_c", 12) == 0; };
     auto other = [&](const Step &st) {
-        return specs_ok && st.launches.size() == 1 && st.pre.empty() && st.launches[0].kind != 3 && !single(st);
+        return specs_ok && st.launches.size() == 1 && st.pre.empty() && st.launches[0].kind < 3 && !single(st);
     };
     auto banded = [&](const Step &st) {
         return specs_ok && st.launches.size() == 2 && st.pre.empty() && st.last - st.first >= 2 &&
@@ -3120,14 +3124,14 @@ void Gpu::pair_launches(const mx_plan_desc *p) {
         // 224x320 GateMms paired too, C4 measured 23.06 -> 23.00 ms/image)
         auto one = [&](size_t u) {
             const Launch &l = *ln[u];
-            return is_pw(l) && l.g[1] == 1 && l.g[2] == 1 && l.g[0] <= (unsigned)(10 * cus);
+            return (is_pw(l) || is_ln(l)) && l.g[1] == 1 && l.g[2] == 1 && l.g[0] <= (unsigned)(10 * cus);
         };
         // the kernel running u and v in one grid (same kernel: its _x2 form;
         // two kernels: A__B_x2, with `swap` when v's blocks come first)
         auto pairfn = [&](size_t u, size_t v, bool &swap) -> hipFunction_t {
             swap = false;
             if (kname(u) == kname(v)) return x2fn(kname(u));
-            if (std::getenv("MAXIM_NO_HPAIR")) return nullptr;
+            if (std::getenv("MAXIM_NO_HPAIR") || !is_pw(*ln[u]) || !is_pw(*ln[v])) return nullptr;
             if (hipFunction_t f = hx2fn(kname(u), kname(v))) return f;
             swap = true;
             return hx2fn(kname(v), kname(u));
@@ -3198,13 +3202,22 @@ void Gpu::pair_launches(const mx_plan_desc *p) {
             d.name = intern(l0.name == l1.name ? std::string(l0.name) + "_x2"
                                                : std::string(l0.name) + "__" + (l1.name + 6) + "_x2");
             d.f = pf;
-            DualGemmArgs da{};
-            memcpy(&da.a, l0.a0, sizeof(GemmArgs));
-            memcpy(&da.b, l1.a0, sizeof(GemmArgs));
-            da.na = l0.g[0];
             d.g[0] = l0.g[0] + l1.g[0];
-            d.kind = 3;
-            set_args(d, da);
+            if (is_ln(l0)) {
+                DualLnArgs dl{};
+                memcpy(&dl.a, l0.a0, sizeof(ChanLnArgs));
+                memcpy(&dl.b, l1.a0, sizeof(ChanLnArgs));
+                dl.na = l0.g[0];
+                d.kind = 4;
+                set_args(d, dl);
+            } else {
+                DualGemmArgs da{};
+                memcpy(&da.a, l0.a0, sizeof(GemmArgs));
+                memcpy(&da.b, l1.a0, sizeof(GemmArgs));
+                da.na = l0.g[0];
+                d.kind = 3;
+                set_args(d, da);
+            }
             st.main = st.launches.size();
             st.launches.push_back(d);
         }

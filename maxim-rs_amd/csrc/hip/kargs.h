@@ -236,6 +236,12 @@ struct DualGemmArgs {
     uint32_t na, pad[3];
 };
 
+// Two LayerNorm launches in one grid, likewise.
+struct DualLnArgs {
+    ChanLnArgs a, b;
+    uint32_t na, pad[3];
+};
+
 // Small GEMV for the plane-1 CALayer convs: y[o] = b[o] + sum_i w[o][i] x[i].
 struct GemvArgs {
     const float *w;

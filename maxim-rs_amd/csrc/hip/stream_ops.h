@@ -207,13 +207,15 @@ extern "C" __global__ __launch_bounds__(MXK_BLOCK) void mx_ca_mean_mlp(CaMeanArg
 
 // STATS: write only the statistics (mean into y[0 .. hw), 1 / std into
 // y[hw .. 2 hw)), for a LayerNorm folded into the next op's GEMM.
+// bx: the block's index among the launch's blocks (a kernel pairing two
+// launches in one grid passes each part its own).
 template <int C, int P, bool STATS = false>
-__device__ void chan_ln_tile(const ChanLnArgs &a) {
+__device__ void chan_ln_tile(const ChanLnArgs &a, int bx) {
     static_assert(C * P <= 8192 && P % 4 == 0 && P <= MXK_BLOCK, "a tile of at most 32 KiB");
     __shared__ float t[C][P];
     __shared__ float st[2][P];
     const int tid = threadIdx.x;
-    const int64_t p0 = (int64_t)blockIdx.x * P;
+    const int64_t p0 = (int64_t)bx * P;
     const bool full = p0 + P <= a.hw;
     constexpr int Q = P / 4;  // float4s per channel row
     for (int i = tid; i < C * Q; i += MXK_BLOCK) {
@@ -343,12 +345,20 @@ __device__ void scale_add_stats_tile(const ScaleAddLnArgs &a) {
 // pixels per block (P = 8192 / C without the suffix); the smaller tiles give
 // small planes more blocks, since each block's serial channel pass is
 // latency-bound.
+// mx_chan_ln_c<C>[_p<P>]_x2: two independent LayerNorms of one shape as one
+// grid (the first d.na blocks run d.a, the rest d.b).
 #define MXK_LN(C, P, SUF)                                                                           \
     extern "C" __global__ __launch_bounds__(MXK_BLOCK) void mx_chan_ln_c##C##SUF(ChanLnArgs a) {    \
-        chan_ln_tile<C, P>(a);                                                                      \
+        chan_ln_tile<C, P>(a, blockIdx.x);                                                          \
+    }                                                                                               \
+    extern "C" __global__ __launch_bounds__(MXK_BLOCK) void mx_chan_ln_c##C##SUF##_x2(DualLnArgs d) { \
+        if (blockIdx.x < d.na)                                                                      \
+            chan_ln_tile<C, P>(d.a, blockIdx.x);                                                    \
+        else                                                                                        \
+            chan_ln_tile<C, P>(d.b, blockIdx.x - d.na);                                             \
     }                                                                                               \
     extern "C" __global__ __launch_bounds__(MXK_BLOCK) void mx_chan_ln_stats_c##C##SUF(ChanLnArgs a) { \
-        chan_ln_tile<C, P, true>(a);                                                                \
+        chan_ln_tile<C, P, true>(a, blockIdx.x);                                                    \
     }                                                                                               \
     extern "C" __global__ __launch_bounds__(MXK_BLOCK) void mx_chan_scale_add_stats_c##C##SUF(ScaleAddLnArgs a) { \
         scale_add_stats_tile<C, P>(a);                                                              \
