@@ -59,9 +59,16 @@ __device__ __forceinline__ float gelu(float x) {
     return __builtin_fmaf(-ax, r, fmaxf(x, 0.0f));
 }
 
-// 1 / (1 + e^-x), the expression of the CPU path's sigmoid (one function, so
-// the standalone kernel, the CALayer block and the fused epilogue agree).
-__device__ __forceinline__ float sigmoid(float x) { return 1.0f / (1.0f + expf(-x)); }
+// 1 / (1 + e^-x) with e^-x = 2^(-x log2 e) on the transcendental unit and
+// one hardware reciprocal (v_exp_f32, v_rcp_f32, 1 ulp each): within
+// 1.3e-7 (1 + |x|) of the exact function, 0 and 1 in the tails where the
+// power overflows or vanishes; held to the CPU path's 1 / (1 + expf(-x))
+// within 4e-7 (1 + |x|). One function, so the standalone kernel, the CALayer
+// block and the fused epilogue agree to the bit.
+__device__ __forceinline__ float sigmoid(float x) {
+    const float e = __builtin_amdgcn_exp2f(-x * 1.4426950408889634f);
+    return __builtin_amdgcn_rcpf(1.0f + e);
+}
 
 // The fused epilogue (kargs.h, Epilogue) for output element `idx`, after bias.
 __device__ __forceinline__ float epilogue(const Epilogue &e, float v, int64_t idx) {

@@ -6,8 +6,9 @@
 // 537-598, 377-434, 1075-1178) and this file is compiled without FP
 // contraction, so add / mul / gate / lrelu / chan_scale / chan_ln /
 // block_perm / down_s / resize reproduce the CPU path bit for bit; sigmoid
-// differs from it only through the device expf, gelu through its erf
-// approximation (common.h, within 2.2e-7 * (1 + |x|) of the exact function).
+// differs from it through its hardware exp2 and reciprocal, gelu through its
+// erf approximation (common.h: within 1.3e-7 and 2.6e-7 * (1 + |x|) of the
+// exact functions).
 #pragma once
 
 #include "common.h"

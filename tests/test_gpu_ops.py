@@ -9,7 +9,8 @@ BIT-EXACT:
 
   exact     copy, add, mul, gate_apply, lrelu, chan_scale, chan_ln,
             block_perm, down_s, resize, and the plane-1 CALayer convs
-  ulps      gelu (A&S 7.1.28 erf vs libm erff), sigmoid (device expf vs libm):
+  ulps      gelu (A&S 7.1.28 erf vs libm erff), sigmoid (hardware exp2 and
+            reciprocal vs libm expf):
             |d| <= 4e-7 * (1 + |x|)
   rounding  chan_mean (tree vs serial order) and every matrix-core GEMM
             (conv1x1, conv3x3, conv4x4s2, convt2x2, gate_mm):
