@@ -110,7 +110,7 @@ def program_walk(plan, img, out=print):
     return D.verify_program_walk(plan, img, O.step, tol=1e-4, out=out)
 
 
-@pytest.mark.parametrize("variant,h,w", [("S-2", 64, 64), ("S-3", 128, 192)])
+@pytest.mark.parametrize("variant,h,w", [("S-2", 64, 64), ("S-3", 128, 192), ("S-3", 64, 320)])
 def test_fused_program_matches_the_cpu_path_step_by_step(gpu_ok, variant, h, w):
     """The program the timed path runs (fused epilogues, folded LayerNorms
     and permutations, split reductions, the default arithmetic order), step
