@@ -318,11 +318,14 @@ __device__ void body(const GemmArgs &a, int ux, int nx, int by, float *xred = nu
             s2.w = s2.w + t2.w;
         }
         // mean, then 1 / std, as the LayerNorm statistics kernels form them
-        const float nf = (float)K;
+        // (K = 128: the product with 1 / K is the quotient to the bit; the
+        // reciprocal square root on the transcendental unit, 1 ulp, where
+        // those kernels divide by a correctly rounded square root)
+        const float inv = 1.0f / (float)K;
         auto stat = [&](float a1, float a2, float &m, float &r) {
-            m = a1 / nf;
-            const float var = a2 / nf - m * m;
-            r = 1.0f / sqrtf(fmaxf(var, 0.0f) + a.ln.eps);
+            m = a1 * inv;
+            const float var = a2 * inv - m * m;
+            r = __builtin_amdgcn_rsqf(fmaxf(var, 0.0f) + a.ln.eps);
         };
         stat(s1.x, s2.x, lmean.x, lrstd.x);
         stat(s1.y, s2.y, lmean.y, lrstd.y);
@@ -579,11 +582,16 @@ __device__ void body(const GemmArgs &a, int ux, int nx, int by, float *xred = nu
                     st4(ly + off, y);
                 }
             };
-            const float nf = (float)(G * TW);
+            // (G TW is a power of two, so the product with its reciprocal is
+            // the quotient to the bit; with the per-wave partial sums, whose
+            // order already differs from the LayerNorm kernels', 1 / std is
+            // the transcendental unit's reciprocal square root, 1 ulp)
+            const float inv = 1.0f / (float)(G * TW);
             auto stats = [&](float s1, float s2, int n_at) {
-                const float m = s1 / nf;
-                const float var = s2 / nf - m * m;
-                const float r = 1.0f / sqrtf(fmaxf(var, 0.0f) + a.lo.eps);
+                const float m = s1 * inv;
+                const float var = s2 * inv - m * m;
+                const float r = a.lo.order ? __builtin_amdgcn_rsqf(fmaxf(var, 0.0f) + a.lo.eps)
+                                           : 1.0f / sqrtf(fmaxf(var, 0.0f) + a.lo.eps);
                 if (a.lo.mode) {  // the statistics only, at the pixel's image position
                     const int n = s0 + n_at;
                     if (n < N) {
