@@ -33,29 +33,27 @@ __device__ __forceinline__ void xcd_tile(int &tile, int &band) {
 __device__ __forceinline__ float4 ld4(const float *p) { return *reinterpret_cast<const float4 *>(p); }
 __device__ __forceinline__ void st4(float *p, float4 v) { *reinterpret_cast<float4 *>(p) = v; }
 
-// GELU, x Phi(x) = 0.5 x (1 + erf(x / sqrt 2)), branch-free, from
-// Abramowitz & Stegun 7.1.28: erfc(z) = (1 + a1 z + ... + a6 z^6)^-16 with
-// |error| <= 3e-7. With z = |x| / sqrt 2 and R = 0.5 erfc(z) = Phi(-|x|),
-// GELU is max(x, 0) - |x| R for either sign of x. The polynomial is taken in
-// |x| (coefficient k scaled by 2^-k/2) and by 2^(1/16) overall, so its 16th
-// power is 2 / (2 R) and one reciprocal gives R: six FMAs, four squarings, a
-// reciprocal, a max and an FMA (the |x| and the sign are source modifiers).
-// Within 2.6e-7 * (1 + |x|) of the exact function; R is 0 once the power
-// overflows. The standalone GELU op and every fused epilogue use this one
-// function, so fusing a GELU changes no bit.
+// GELU, x Phi(x) = 0.5 x (1 + erf(x / sqrt 2)), branch-free: with
+// R = Phi(-|x|), GELU is max(x, 0) - |x| R for either sign of x, and
+// R = 2^q(t) at t = min(|x|, 6), q the degree-6 polynomial fitted by
+// weighted least squares to log2 Phi(-t) over [0, 6] (each point weighted by
+// how little error its GELU value allows, so the fit is tightest near 0),
+// evaluated by Horner and raised on the transcendental unit (v_exp_f32, 1
+// ulp): a min, six FMAs, one exp2, a max and an FMA (the |x| and the sign
+// are source modifiers). Within 6.3e-8 * (1 + |x|) of the exact function
+// (past |x| = 6 the clamped R is below 1e-9). The standalone GELU op and
+// every fused epilogue use this one function, so fusing a GELU changes no
+// bit.
 __device__ __forceinline__ float gelu(float x) {
     const float ax = fabsf(x);
-    float t = __builtin_fmaf(5.621299806e-06f, ax, 5.105520904e-05f);
-    t = __builtin_fmaf(t, ax, 3.968613601e-05f);
-    t = __builtin_fmaf(t, ax, 3.422739217e-03f);
-    t = __builtin_fmaf(t, ax, 2.207699791e-02f);
-    t = __builtin_fmaf(t, ax, 5.207516253e-02f);
-    t = __builtin_fmaf(t, ax, 1.044273734e+00f);
-    t = t * t;
-    t = t * t;
-    t = t * t;
-    t = t * t;
-    const float r = __builtin_amdgcn_rcpf(t);  // Phi(-|x|)
+    const float t = fminf(ax, 6.0f);
+    float q = __builtin_fmaf(3.3113869e-05f, t, -7.6996483e-04f);
+    q = __builtin_fmaf(q, t, 8.0852984e-03f);
+    q = __builtin_fmaf(q, t, -5.3423237e-02f);
+    q = __builtin_fmaf(q, t, -4.5875868e-01f);
+    q = __builtin_fmaf(q, t, -1.1512076e+00f);
+    q = __builtin_fmaf(q, t, -9.9999213e-01f);
+    const float r = __builtin_amdgcn_exp2f(q);  // Phi(-|x|)
     return __builtin_fmaf(-ax, r, fmaxf(x, 0.0f));
 }
 

@@ -7,7 +7,7 @@
 // contraction, so add / mul / gate / lrelu / chan_scale / chan_ln /
 // block_perm / down_s / resize reproduce the CPU path bit for bit; sigmoid
 // differs from it through its hardware exp2 and reciprocal, gelu through its
-// erf approximation (common.h: within 1.3e-7 and 2.6e-7 * (1 + |x|) of the
+// fitted exponent (common.h: within 1.3e-7 and 6.3e-8 * (1 + |x|) of the
 // exact functions).
 #pragma once
 

@@ -75,7 +75,8 @@ def gpu_ok():
 # Per-op bars of the lockstep walks (the reference's --verify-gpu uses
 # max|d| <= 1e-3 * max|cpu| for every op, src/main.rs:709-712):
 #   exact     ops whose arithmetic the executor reproduces term for term
-#   ulps      gelu (A&S 7.1.28 erf vs libm erff), sigmoid (device expf vs libm):
+#   ulps      gelu (fitted exp2 polynomial vs libm erff), sigmoid (hardware exp2
+#             and reciprocal vs libm expf):
 #             |d| <= 4e-7 * (1 + |x|)
 #   rounding  chan_mean and every matrix-core GEMM: max|d| <= 1e-4 * max|cpu|
 EXACT = {"copy", "add", "mul", "gate_apply", "lrelu", "chan_scale", "chan_ln", "block_perm",

@@ -9,7 +9,7 @@ BIT-EXACT:
 
   exact     copy, add, mul, gate_apply, lrelu, chan_scale, chan_ln,
             block_perm, down_s, resize, and the plane-1 CALayer convs
-  ulps      gelu (A&S 7.1.28 erf vs libm erff), sigmoid (hardware exp2 and
+  ulps      gelu (fitted exp2 polynomial vs libm erff), sigmoid (hardware exp2 and
             reciprocal vs libm expf):
             |d| <= 4e-7 * (1 + |x|)
   rounding  chan_mean (tree vs serial order) and every matrix-core GEMM
