@@ -2707,7 +2707,9 @@ void Gpu::build_program(const mx_plan_desc *p) {
                 a.N = (int32_t)(r.h * r.wd);
                 a.C = scratch + rs_off;
                 Launch g;
-                if (a.batch == 1 && a.M == c.c_out && try_pw(0, a, g)) {
+                // (the 256-column forms store 128 bits: the conv's output must be 16-byte aligned)
+                const bool st_ok = strncmp(rl[0].name, "mx_resize_hv4", 13) != 0 || aligned(out, 16);
+                if (a.batch == 1 && a.M == c.c_out && st_ok && try_pw(0, a, g)) {
                     Resize2Args z;
                     memcpy(&z, rl[0].a0, sizeof z);
                     z.x = scratch + rs_off;
