@@ -196,3 +196,45 @@ def test_split_gemm_layernorm_statistics(gpu_ok, h, w):
     plain, _ = go(False)
     assert any(k.startswith("mx_chan_ln_stats") for k in ks2), ks2
     assert np.array_equal(kept.view(np.uint32), plain.view(np.uint32))
+
+
+def test_commuted_pair_into_a_misaligned_output(gpu_ok):
+    """The commuted pair's resize writes the conv's output, and the 256-column
+    resize stores 128 bits: with that output one float off a 16-byte
+    boundary the pair runs in the plan's order instead (the plan-order resize
+    writes its own, aligned output), bit-equal to the op-by-op pass and within
+    the GEMM bar of the CPU path."""
+    from maxim_amd import plan as P
+    from maxim_amd import hip as H
+    from oracle import oracle as O
+    ci, h, w, oh, ow, co = 64, 30, 44, 60, 88, 16
+    rng = np.random.default_rng(9)
+    wt = (rng.standard_normal((co, ci)) * np.sqrt(2.0 / ci)).astype(np.float32)
+    b = rng.normal(0, 0.1, co).astype(np.float32)
+    ops = [P.make_op(P.RESIZE, dst=2, src=0, src2=1, c=ci, h=h, wd=w, oh=oh, ow=ow),
+           P.make_op(P.CONV1X1, dst=4, src=2, w=0, bias=1, c_in=ci, c_out=co, h=oh, wd=ow)]
+    bufs = [(ci, h, w), (ci, h, ow), (ci, oh, ow), (1, 1, 1), (co, oh, ow)]
+    cp = P.CustomPlan(bufs, ops, [wt.ravel(), b], input=0, output=4, align=1)
+    assert int(cp.offs[2]) % 4 == 0 and int(cp.offs[4]) % 4 == 1
+    x = rng.standard_normal((ci, h, w)).astype(np.float32)
+    out = {}
+    for fused in (True, False):
+        gpu = H.Gpu(cp)
+        assert gpu.buf_offset(4) % 4 == 1  # elements: 4 bytes past a 16-byte boundary
+        gpu.set_fusion(fused)
+        gpu.write_buf(0, x)
+        gpu.run_ops(0, len(cp.ops))
+        out[fused] = (gpu.read_buf(4).reshape(co, oh, ow), [k for _, k in gpu.launches()])
+        gpu.close()
+    got, kernels = out[True]
+    print("kernels", kernels, flush=True)
+    # the plan's order: the resize first (the conv then takes a kernel that
+    # stores to any 4-byte boundary)
+    assert len(kernels) == 2 and kernels[0].startswith("mx_resize_hv4_"), kernels
+    assert np.array_equal(got.view(np.uint32), out[False][0].view(np.uint32))
+    arena = np.zeros(cp.arena_len, np.float32)
+    arena[:x.size] = x.ravel()
+    O.run(cp, arena)
+    o = int(cp.offs[4])
+    ref = arena[o:o + co * oh * ow].reshape(co, oh, ow).astype(np.float64)
+    assert float(np.abs(got - ref).max()) <= 1e-4 * float(np.abs(ref).max())
